@@ -1,0 +1,164 @@
+/*
+ * libllmembed_hip.so — MI355X (gfx950) encoder forward pass for nomic-bert GGUF models.
+ *
+ * C ABI only: integers, pointers and sizes; floats travel as u32 bit patterns inside
+ * structs (the reference's Windows MKL bridge passes every argument as a pointer for
+ * the same reason: internal/ggml/mkl_windows.go:45,64-118). No torch / HIP types appear
+ * in any signature; `stream` arguments are opaque hipStream_t values (NULL = the model's
+ * own stream).
+ *
+ * Contract (mirrors what the reference's callers rely on):
+ *   - Every entry point is re-entrant and callable from any OS thread; the device is set
+ *     per call. Calls on one model are serialised internally (one forward at a time).
+ *   - Host pointers are read or written only during the call; the library keeps none.
+ *   - Host-pointer entry points are synchronous on return.
+ *   - Return value: 0 on success, a negative LLE_E* code on failure; lle_last_error()
+ *     returns a thread-local message for the last failure on the calling thread.
+ */
+#ifndef LLMEMBED_H
+#define LLMEMBED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLE_ABI_VERSION 1
+
+#define LLE_OK 0
+#define LLE_EINVAL (-1)       /* bad argument, shape or id */
+#define LLE_EDEVICE (-2)      /* no usable gfx950 device, or a HIP runtime failure */
+#define LLE_ENOMEM (-3)       /* device allocation failed */
+#define LLE_EUNSUPPORTED (-4) /* ggml type / model shape the path does not handle */
+#define LLE_EIO (-5)          /* file open / read / parse failure */
+#define LLE_ENOTFOUND (-6)    /* a required GGUF tensor or key is missing */
+
+/* GGML tensor type ids (internal/gguf/reader.go:49-66). */
+#define LLE_TYPE_F32 0
+#define LLE_TYPE_Q8_0 8
+#define LLE_TYPE_Q4_K 12
+#define LLE_TYPE_Q5_K 13
+#define LLE_TYPE_Q6_K 14
+
+typedef struct lle_model lle_model;
+typedef struct lle_weight lle_weight;
+
+/* One GGUF tensor as it sits in the file: dims[0] = ne0 = inner K, ne1 = rows.
+ * Replaces *ggml.Tensor{Name, Shape, Type, Data} (internal/ggml/tensor.go:13-18). */
+typedef struct {
+  int32_t type;
+  int64_t ne0;
+  int64_t ne1;
+  const void* data;
+  int64_t nbytes;
+} lle_tensor;
+
+/* Model description. Replaces BertModel's fields (internal/embed/bert.go:14-43,54-87) as
+ * filled by LoadBertModel (:91-212); ln_eps / rope_base are float32 bit patterns. */
+typedef struct {
+  int32_t n_layer, d_model, n_head, d_ff, max_seq;
+  uint32_t ln_eps_bits, rope_base_bits;
+  lle_tensor token_embd, token_types, embd_norm_w, embd_norm_b;
+  /* arrays of n_layer tensors each */
+  const lle_tensor* qkv;
+  const lle_tensor* out;
+  const lle_tensor* attn_norm_w;
+  const lle_tensor* attn_norm_b;
+  const lle_tensor* up;
+  const lle_tensor* gate;
+  const lle_tensor* down;
+  const lle_tensor* out_norm_w;
+  const lle_tensor* out_norm_b;
+} lle_model_desc;
+
+/* Per-kernel-class timing collected with HIP events on the forward's stream. */
+typedef struct {
+  char name[32];
+  int64_t launches;
+  double total_ms;
+  double flops; /* algorithmic FLOPs summed over launches */
+  double bytes; /* algorithmic HBM bytes summed over launches */
+} lle_kernel_time;
+
+int32_t lle_abi_version(void);
+
+/* Select and probe a device (gfx950 required). Replaces the MKL dlopen probe
+ * initMKL (internal/ggml/mkl_linux.go:45-61): a failure here is what makes a host
+ * fall back to its CPU path, as useMKL=false does. */
+int32_t lle_init(int32_t device_ordinal);
+
+const char* lle_last_error(void);
+
+/* Human-readable backend description; SgemmInfo analogue (internal/ggml/sgemm.go:263-269). */
+int32_t lle_info(char* buf, int32_t cap);
+
+/* Test hook: f16 bit patterns -> f32 on the device, bit-exact with f16ToF32
+ * (internal/ggml/tensor.go:162-191), NaN payloads included. */
+int32_t lle_f16_to_f32(const uint16_t* h, int64_t n, float* out);
+
+/* Test hook: dequantise raw GGUF blocks on the device; the same values as
+ * Tensor.Dequantize / DequantWeightMatrix (internal/ggml/tensor.go:51-66,
+ * internal/ggml/gemm.go:221-267), bit for bit. */
+int32_t lle_dequant(int32_t ggml_type, const void* blocks, int64_t n_elements, float* out);
+
+/* Upload a model: LoadBertModel + PreDequant + NewRoPETable
+ * (internal/embed/bert.go:91-212,542-576; internal/ggml/ops_simd.go:107-124).
+ * Weights stay quantised in HBM (bit-preserving re-layout); no host pointer is kept. */
+int32_t lle_model_create(const lle_model_desc* desc, lle_model** out);
+
+/* Parse a GGUF file and upload it (internal/gguf/reader.go:219-280 + the above). */
+int32_t lle_model_load_gguf(const char* path, lle_model** out);
+
+int32_t lle_model_destroy(lle_model* m);
+
+/* dims[0..6] = n_layer, d_model, n_head, d_ff, max_seq, vocab. */
+int32_t lle_model_dims(const lle_model* m, int32_t* dims);
+
+/* Embed one sequence (Embedder.Embed after tokenisation, internal/embed/embedder.go:46-71):
+ * forward + masked mean-pool + L2 (+ Matryoshka truncate/renormalise when out_dim < d_model).
+ * out: min(out_dim, d_model) floats. */
+int32_t lle_embed(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t L, int32_t out_dim,
+                  float* out);
+
+/* Batched embed: B right-padded rows of length L (mask 1 = token, 0 = padding). Each row's
+ * result equals lle_embed on that row bit for bit (batch invariance, as the reference's
+ * EmbedBatch == Embed tests require: internal/embed/embedder_test.go:139-144,246-251).
+ * out: B x min(out_dim, d_model). */
+int32_t lle_embed_batch(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L,
+                        int32_t out_dim, float* out);
+
+/* Same on device pointers, enqueued on `stream` (NULL = the model's stream); returns after
+ * enqueueing. Token ids outside [0, vocab) are clamped and reported by lle_model_status. */
+int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int32_t B,
+                              int32_t L, int32_t out_dim, float* d_out, void* stream);
+
+/* Parity hook: hidden states [B*L][d_model] before pooling (BertModel.Forward output,
+ * internal/embed/bert.go:216-285). */
+int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L,
+                           float* hidden);
+
+/* Device-side status word of the last async forward: 0 ok, 1 = a token id was out of range. */
+int32_t lle_model_status(lle_model* m, int32_t* status);
+
+/* Kernel timing: enable (1) / disable (0) and read per-kernel-class HIP-event totals. */
+int32_t lle_model_set_timing(lle_model* m, int32_t enable);
+int32_t lle_model_get_timing(lle_model* m, lle_kernel_time* out, int32_t cap, int32_t* n_out);
+
+/* Isolated quantised projection (gemmOrBatch, internal/embed/bert.go:579-638):
+ * Y[M][N] = X[M][K] . W^T, W one GGUF tensor [K, N] (N rows of K, blocks along K). */
+int32_t lle_weight_create(int32_t ggml_type, const void* blocks, int32_t K, int32_t N, lle_weight** out);
+int32_t lle_weight_destroy(lle_weight* w);
+/* Test hook: the uploaded (re-laid-out) weight dequantised by the GEMM's own decoder,
+ * as f32 [N][K] (must equal DequantWeightMatrix bit for bit). */
+int32_t lle_weight_dequant(const lle_weight* w, float* out);
+/* Host pointers, synchronous. */
+int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y);
+/* Device pointers: X f32 [M][K] is converted to f16 into d_x16 (M*K halfs, caller-owned),
+ * then Y f32 [M][N]; enqueued on stream. */
+int32_t lle_gemm_async(const lle_weight* w, const float* d_X, void* d_x16, int32_t M, float* d_Y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,242 @@
+// Bidirectional masked multi-head attention with the reference's softmax semantics, on MFMA.
+//
+// Reference: internal/embed/bert.go:356-402 with DotF32 / SoftmaxInPlace / fastExp
+// (internal/ggml/ops_simd.go:46-97):
+//   s = (q . k) * 1/sqrt(64);  mask[key] == 0  ->  s = -1e9 (assigned);
+//   m = max s;  e = (s - m < -10) ? 0 : exp(s - m);  p = e / sum e;  o = sum p v.
+// One block = 64 queries of one (sequence, head); 4 waves x 16 queries. Keys stream through
+// LDS 64 at a time; S = K Q^T and O^T = V^T P^T run on v_mfma_f32_16x16x32_f16.
+//
+// Cutoff with an online max: a key is kept when s - m_run >= -10, with m_run the running max.
+// Every key the reference keeps is kept (m_run <= m_final). A kept key the reference would drop
+// has s - m_final < -10; the smallest kept score per query detects that case after the pass,
+// and the block then repeats the pass with m_final fixed, which is exactly the reference rule.
+// Key tiles outside [first valid key, last valid key] hold only masked keys; they contribute
+// exact zeros and are skipped (all tiles are visited when a sequence has no valid key, where
+// the reference's softmax is uniform).
+//
+// S-tile row permutation: S tile t row 4g+r holds key 32*(t/2) + 8g + 4*(t%2) + r, so the
+// lane that owns rows 4g..4g+3 of tiles 2j and 2j+1 owns keys 32j + 8g .. 32j + 8g + 7 —
+// exactly the 8 consecutive keys its B operand of the P.V MFMA needs. No cross-lane traffic.
+#include "lle_internal.h"
+
+namespace lle {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int AQ = 64;   // queries per block
+constexpr int AK = 64;   // keys per tile
+constexpr int HD = 64;   // head dim
+constexpr int APAD = 8;
+
+__global__ void kv_range_kernel(const int32_t* __restrict__ mask, int L, int32_t* __restrict__ range) {
+  const int b = blockIdx.x;
+  int lo = L, hi = -1;
+  for (int i = threadIdx.x; i < L; i += blockDim.x) {
+    if (mask[(size_t)b * L + i] != 0) {
+      lo = min(lo, i);
+      hi = max(hi, i);
+    }
+  }
+  __shared__ int slo[256], shi[256];
+  slo[threadIdx.x] = lo;
+  shi[threadIdx.x] = hi;
+  __syncthreads();
+  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      slo[threadIdx.x] = min(slo[threadIdx.x], slo[threadIdx.x + s]);
+      shi[threadIdx.x] = max(shi[threadIdx.x], shi[threadIdx.x + s]);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (shi[0] < 0) {  // no valid key: uniform softmax over all L keys
+      range[2 * b] = 0;
+      range[2 * b + 1] = L;
+    } else {
+      range[2 * b] = slo[0];
+      range[2 * b + 1] = shi[0] + 1;
+    }
+  }
+}
+
+hipError_t launch_kv_range(const int32_t* mask, int B, int L, int32_t* kv_range, hipStream_t st) {
+  hipLaunchKernelGGL(kv_range_kernel, dim3(B), dim3(256), 0, st, mask, L, kv_range);
+  return hipGetLastError();
+}
+
+__device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 sK[AK][HD + APAD];   // [key][dim]
+  __shared__ __attribute__((aligned(16))) _Float16 sV[HD][AK + APAD];   // [dim][key]
+  __shared__ int sMask[AK];
+  __shared__ int sRedo;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, lr = lane & 15;
+  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int L = a.L, Lp = a.Lp, H = a.H;
+  const size_t head = (size_t)b * H + h;
+  const int q = qt * AQ + wave * 16 + lr;
+
+  // Q^T fragments (B operand of S): query q, dims ks*32 + 8g .. +7
+  half8 qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    if (q < L)
+      qf[ks] = *(const half8*)(a.q + (head * Lp + q) * HD + ks * 32 + g * 8);
+    else
+      qf[ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  const int klo = a.kv_range[2 * b], khi = a.kv_range[2 * b + 1];
+  const int t0 = klo / AK, t1 = (khi + AK - 1) / AK;
+  const float scale = 0.125f;  // float32(1/sqrt(64)), bert.go:362
+
+  float m_run = -INFINITY, lsum = 0.f, smin = INFINITY;
+  floatx4 o[4];
+
+  if (tid == 0) sRedo = 0;
+  for (int pass = 0; pass < 2; pass++) {
+    const bool fixed = pass == 1;
+    if (fixed) {
+      __syncthreads();
+      if (!sRedo) break;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    lsum = 0.f;
+    smin = INFINITY;
+    const float m_fix = m_run;
+
+    for (int kt = t0; kt < t1; kt++) {
+      __syncthreads();
+      // K tile: 64 keys x 64 dims, and V^T tile: 64 dims x 64 keys
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int c = tid + i * 256, row = c >> 3, ch = c & 7;
+        const int key = kt * AK + row;
+        uint4 kv = uint4{0, 0, 0, 0};
+        if (key < L) kv = *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8);
+        *(uint4*)&sK[row][ch * 8] = kv;
+        const int k0 = kt * AK + ch * 8;
+        uint4 vv = uint4{0, 0, 0, 0};
+        if (k0 < L) {
+          vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
+          if (k0 + 8 > L) {
+            _Float16* e = (_Float16*)&vv;
+            for (int j = L - k0; j < 8; j++) e[j] = (_Float16)0.f;
+          }
+        }
+        *(uint4*)&sV[row][ch * 8] = vv;
+      }
+      if (tid < AK) {
+        const int key = kt * AK + tid;
+        sMask[tid] = key < L ? a.mask[(size_t)b * L + key] : 0;
+      }
+      __syncthreads();
+
+      // S^T tiles: st[t][r] = score of key kidx(t, r) for query q
+      floatx4 st[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int krow = 32 * (t >> 1) + 8 * (lr >> 2) + 4 * (t & 1) + (lr & 3);
+        floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+          const half8 kf = *(const half8*)&sK[krow][ks * 32 + g * 8];
+          acc = mfma16(kf, qf[ks], acc);
+        }
+        st[t] = acc;
+      }
+      float s[16];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int kl = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;
+          float v = st[t][r] * scale;
+          if (sMask[kl] == 0) v = -1e9f;  // masked (and out-of-range) keys
+          s[4 * t + r] = v;
+          tmax = fmaxf(tmax, v);
+        }
+      float alpha = 1.f, mref;
+      if (!fixed) {
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run, tmax);
+        alpha = (m_new == m_run) ? 1.f : __expf(m_run - m_new);
+        m_run = m_new;
+        mref = m_new;
+      } else {
+        mref = m_fix;
+      }
+      float e[16];
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float z = s[i] - mref;
+        if (z < -10.f) {
+          e[i] = 0.f;
+        } else {
+          e[i] = __expf(z);
+          smin = fminf(smin, s[i]);
+        }
+        ps += e[i];
+      }
+      lsum = lsum * alpha + ps;
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+      // P^T fragments: keys 32j + 8g + 0..7
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        half8 pf;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          pf[r] = (_Float16)e[4 * (2 * j) + r];
+          pf[4 + r] = (_Float16)e[4 * (2 * j + 1) + r];
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+          const half8 vf = *(const half8*)&sV[dt * 16 + lr][32 * j + 8 * g];
+          o[dt] = mfma16(vf, pf, o[dt]);
+        }
+      }
+    }
+    if (!fixed) {
+      float sm = fminf(smin, __shfl_xor(smin, 16));
+      sm = fminf(sm, __shfl_xor(sm, 32));
+      const bool flag = (q < L) && (sm - m_run < -10.f);
+      if (__any(flag)) sRedo = 1;  // benign race: every writer stores 1
+    }
+  }
+
+  float tot = lsum + __shfl_xor(lsum, 16);
+  tot += __shfl_xor(tot, 32);
+  if (q < L) {
+    const float inv = 1.f / tot;
+    __half* dst = a.out + ((size_t)b * L + q) * a.D + h * HD + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+      __half2 lo = __floats2half2_rn(o[dt][0] * inv, o[dt][1] * inv);
+      __half2 hi = __floats2half2_rn(o[dt][2] * inv, o[dt][3] * inv);
+      uint2 pk;
+      pk.x = *(uint32_t*)&lo;
+      pk.y = *(uint32_t*)&hi;
+      *(uint2*)(dst + dt * 16) = pk;
+    }
+  }
+}
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
+  dim3 grid((a.L + AQ - 1) / AQ, a.H, a.B);
+  hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace lle

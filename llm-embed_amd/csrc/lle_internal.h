@@ -1,0 +1,121 @@
+// Internal declarations shared by the HIP kernels and the host runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/llmembed.h"
+
+namespace lle {
+
+// ---------------------------------------------------------------------------------------
+// Error plumbing (thread-local last error, negative codes).
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+#define LLE_HIP(call)                                                                  \
+  do {                                                                                 \
+    hipError_t e_ = (call);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return ::lle::fail(LLE_EDEVICE, std::string(#call) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------
+// Device-resident weight formats. Every format is a bit-preserving re-layout of the GGUF
+// blocks into "k-group major" planes so that one 64-wide K step of BN consecutive rows is a
+// contiguous, 16-byte aligned run per plane. Bytes per weight are exactly the GGUF ones.
+//
+//   Q8_0 : codes [K/32][N][32] int8       scales [K/32][N] f16 bits
+//   Q4_K : qs    [K/64][N][32] (low nibble = element l, high = element 32+l of the group)
+//          hdr   [K/256][N][16] = GGUF {d, dmin, scales[12]} verbatim
+//   Q5_K : qs, hdr as Q4_K;  qh [K/64][N][2] u32: word w bit l = high bit of element 32w+l
+//   Q6_K : ql    [K/64][N][32] (low nibble = element l, high = element 32+l), 4-bit low parts
+//          qh    [K/64][N][16] (element e: byte e/4, bits 2(e%4)..+1), 2-bit high parts
+//          sc    [K/64][N][4]  int8 scale of elements 16s..16s+15 of the group
+//          d     [K/256][N]    f16 bits
+//   F32  : [N][K] f32
+struct WeightDev {
+  int type = -1;
+  int K = 0, N = 0;
+  void* base = nullptr;  // one allocation holding every plane
+  size_t bytes = 0;      // algorithmic bytes (= GGUF bytes)
+  const uint8_t* p0 = nullptr;  // codes / qs / ql / f32
+  const uint8_t* p1 = nullptr;  // scales / hdr / qh
+  const uint8_t* p2 = nullptr;  // qh (Q5_K) / sc (Q6_K)
+  const uint8_t* p3 = nullptr;  // d (Q6_K)
+};
+
+// Host-side re-layout of GGUF blocks of a [N][K] matrix into the planes above.
+size_t weight_dev_bytes(int type, int K, int N);  // algorithmic (GGUF) bytes
+void plane_offsets(int type, int K, int N, size_t off[4], size_t* total);
+void repack_rows(int type, const uint8_t* gguf, int K, int N, uint8_t* dst, const size_t off[4]);
+
+// ---------------------------------------------------------------------------------------
+// Kernel launchers (defined in the .hip files). All enqueue on `st` and return hipError_t.
+
+enum Epilogue { EPI_F32 = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GEGLU = 3 };
+
+struct GemmArgs {
+  const WeightDev* w;
+  const __half* x;  // [M][K] f16
+  int M;
+  // EPI_F32: y f32 [M][N]; EPI_RESID: y f32 [M][N] (+=)
+  float* y;
+  // EPI_QKV: q/k [B][H][Lp][64] f16, vt [B][H][64][Lp] f16
+  __half* q;
+  __half* k;
+  __half* vt;
+  const float* rope_cos;  // [max_seq][32]
+  const float* rope_sin;
+  int L, Lp, n_head, d_model;
+  // EPI_GEGLU: out f16 [M][N/2]
+  __half* g;
+  // split-K partials for M <= 64: [K/256][M][N] f32
+  float* part;
+};
+
+hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st);
+
+hipError_t launch_f32_to_f16(const float* x, __half* y, int64_t n, hipStream_t st);
+hipError_t launch_f16_to_f32_bits(const uint16_t* h, float* out, int64_t n, hipStream_t st);
+hipError_t launch_dequant_raw(int type, const uint8_t* blocks, int64_t n, float* out, hipStream_t st);
+hipError_t launch_dequant_weight(const WeightDev& w, float* out, hipStream_t st);
+
+struct EmbedArgs {
+  const int32_t* ids;
+  int T;
+  int vocab;
+  int tok_type;
+  const uint8_t* tok;  // raw GGUF token_embd
+  int64_t tok_row_bytes;
+  const float* type0;  // [D]
+  const float* w;
+  const float* b;
+  float eps;
+  int D;
+  float* h;
+  __half* h16;
+  int32_t* status;
+};
+hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st);
+hipError_t launch_ln(float* h, __half* h16, const float* w, const float* b, float eps, int T, int D,
+                     hipStream_t st);
+
+struct AttnArgs {
+  const __half* q;
+  const __half* k;
+  const __half* vt;
+  const int32_t* mask;   // [B][L]
+  const int32_t* kv_range;  // [B][2] key tile range [lo, hi) in keys
+  __half* out;           // [B*L][D]
+  int B, L, Lp, H, D;
+};
+hipError_t launch_kv_range(const int32_t* mask, int B, int L, int32_t* kv_range, hipStream_t st);
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+
+hipError_t launch_pool(const float* h, const int32_t* mask, int B, int L, int D, int out_dim, float* out,
+                       hipStream_t st);
+
+}  // namespace lle

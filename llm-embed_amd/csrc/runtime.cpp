@@ -1,0 +1,806 @@
+// Host runtime of libllmembed_hip.so: device probe, model upload, forward orchestration and
+// the C-ABI entry points declared in include/llmembed.h.
+//
+// Mirrors the reference's model lifecycle:
+//   LoadBertModel + PreDequant + NewRoPETable (internal/embed/bert.go:91-212,542-576,
+//   internal/embed/embedder.go:19-42)  ->  lle_model_create / lle_model_load_gguf
+//   Embed / EmbedBatch (internal/embed/embedder.go:46-133)  ->  lle_embed / lle_embed_batch
+//   BertModel.Forward (internal/embed/bert.go:216-285)      ->  forward() below
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "lle_internal.h"
+
+namespace lle {
+
+static thread_local std::string g_err;
+void set_error(const std::string& m) { g_err = m; }
+int fail(int code, const std::string& m) {
+  g_err = m;
+  return code;
+}
+
+static int g_device = -1;
+static std::mutex g_init_mu;
+
+static int64_t row_bytes(int type, int64_t n) {
+  switch (type) {
+    case 0: return n * 4;
+    case 8: return (n / 32) * 34;
+    case 12: return (n / 256) * 144;
+    case 13: case 15: case 16: return (n / 256) * 176;
+    case 14: return (n / 256) * 210;
+    default: return -1;
+  }
+}
+
+static int ensure_init() {
+  if (g_device >= 0) return LLE_OK;
+  return lle_init(0);
+}
+
+struct Timer {
+  std::string name;
+  hipEvent_t a, b;
+  double flops, bytes;
+};
+
+struct Layer {
+  WeightDev qkv, out, upgate, down;
+  float *anw = nullptr, *anb = nullptr, *onw = nullptr, *onb = nullptr;
+};
+
+}  // namespace lle
+
+struct lle_weight {
+  lle::WeightDev w;
+  int device = 0;
+  hipStream_t stream = nullptr;
+};
+
+struct lle_model {
+  int device = 0;
+  int n_layer = 0, D = 0, H = 0, F = 0, max_seq = 0, vocab = 0;
+  float eps = 0.f, rope_base = 0.f;
+  uint8_t* tok = nullptr;
+  int tok_type = 0;
+  int64_t tok_row_bytes = 0;
+  float *type0 = nullptr, *enw = nullptr, *enb = nullptr;
+  std::vector<lle::Layer> layers;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  std::vector<void*> allocs;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  // workspace
+  size_t ws_T = 0, ws_heads = 0, ws_part = 0;
+  int ws_B = 0;
+  float* h = nullptr;
+  __half* h16 = nullptr;
+  __half *q = nullptr, *k = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
+  float* part = nullptr;
+  int32_t *ids = nullptr, *mask = nullptr, *kv_range = nullptr, *status = nullptr;
+  float* out = nullptr;
+  // timing
+  bool timing = false;
+  std::vector<lle::Timer> pending;
+  std::vector<lle_kernel_time> totals;
+  std::vector<hipEvent_t> event_pool;
+};
+
+namespace lle {
+
+static int dev_alloc(lle_model* m, void** p, size_t bytes) {
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return fail(LLE_ENOMEM, std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(e));
+  m->allocs.push_back(*p);
+  return LLE_OK;
+}
+
+static void ws_free(lle_model* m) {
+  void* bufs[] = {m->h, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->kv_range, m->out};
+  for (void* b : bufs)
+    if (b) (void)hipFree(b);
+  m->h = nullptr; m->h16 = nullptr; m->q = m->k = m->vt = m->attn = m->ff = nullptr;
+  m->part = nullptr; m->ids = m->mask = m->kv_range = nullptr; m->out = nullptr;
+  m->ws_T = m->ws_heads = m->ws_part = 0;
+  m->ws_B = 0;
+}
+
+#define WS_ALLOC(ptr, bytes)                                                            \
+  do {                                                                                  \
+    void* p_ = nullptr;                                                                 \
+    hipError_t e_ = hipMalloc(&p_, (bytes) ? (bytes) : 256);                            \
+    if (e_ != hipSuccess) {                                                             \
+      ws_free(m);                                                                       \
+      return fail(LLE_ENOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e_)); \
+    }                                                                                   \
+    ptr = (decltype(ptr))p_;                                                            \
+  } while (0)
+
+// Grow-only workspace for a [B][L] batch.
+static int ensure_ws(lle_model* m, int B, int L) {
+  const size_t T = (size_t)B * L;
+  const int Lp = (L + 63) / 64 * 64;
+  const size_t heads = (size_t)B * m->H * Lp * 64;
+  const size_t kd = (size_t)m->D / 256, kf = (size_t)m->F / 256;
+  const size_t part = T <= 64 ? (size_t)64 * std::max({kd * 3 * m->D, kd * 2 * m->F, kf * m->D}) : 0;
+  if (T <= m->ws_T && heads <= m->ws_heads && part <= m->ws_part && B <= m->ws_B) return LLE_OK;
+  const size_t nT = std::max(T, m->ws_T), nH = std::max(heads, m->ws_heads), nP = std::max(part, m->ws_part);
+  const int nB = std::max(B, m->ws_B);
+  LLE_HIP(hipStreamSynchronize(m->stream));
+  ws_free(m);
+  WS_ALLOC(m->h, nT * m->D * 4);
+  WS_ALLOC(m->h16, nT * m->D * 2);
+  WS_ALLOC(m->q, nH * 2);
+  WS_ALLOC(m->k, nH * 2);
+  WS_ALLOC(m->vt, nH * 2);
+  WS_ALLOC(m->attn, nT * m->D * 2);
+  WS_ALLOC(m->ff, nT * m->F * 2);
+  if (nP) WS_ALLOC(m->part, nP * 4);
+  WS_ALLOC(m->ids, nT * 4);
+  WS_ALLOC(m->mask, nT * 4);
+  WS_ALLOC(m->kv_range, (size_t)nB * 8);
+  WS_ALLOC(m->out, (size_t)nB * m->D * 4);
+  m->ws_T = nT;
+  m->ws_heads = nH;
+  m->ws_part = nP;
+  m->ws_B = nB;
+  return LLE_OK;
+}
+
+static hipEvent_t get_event(lle_model* m) {
+  if (!m->event_pool.empty()) {
+    hipEvent_t e = m->event_pool.back();
+    m->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  (void)hipEventCreate(&e);
+  return e;
+}
+
+struct Scope {
+  lle_model* m;
+  hipStream_t st;
+  Timer t;
+  bool on;
+  Scope(lle_model* m_, hipStream_t st_, const char* name, double flops, double bytes) : m(m_), st(st_), on(m_->timing) {
+    if (on) {
+      t.name = name;
+      t.flops = flops;
+      t.bytes = bytes;
+      t.a = get_event(m);
+      t.b = get_event(m);
+      (void)hipEventRecord(t.a, st);
+    }
+  }
+  ~Scope() {
+    if (on) {
+      (void)hipEventRecord(t.b, st);
+      m->pending.push_back(t);
+    }
+  }
+};
+
+static void collect_timing(lle_model* m) {
+  for (auto& t : m->pending) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, t.a, t.b) != hipSuccess) ms = 0.f;
+    auto it = std::find_if(m->totals.begin(), m->totals.end(),
+                           [&](const lle_kernel_time& k) { return t.name == k.name; });
+    if (it == m->totals.end()) {
+      lle_kernel_time k;
+      memset(&k, 0, sizeof(k));
+      snprintf(k.name, sizeof(k.name), "%s", t.name.c_str());
+      m->totals.push_back(k);
+      it = m->totals.end() - 1;
+    }
+    it->launches += 1;
+    it->total_ms += ms;
+    it->flops += t.flops;
+    it->bytes += t.bytes;
+    m->event_pool.push_back(t.a);
+    m->event_pool.push_back(t.b);
+  }
+  m->pending.clear();
+}
+
+#define LAUNCH(expr)                                                                 \
+  do {                                                                               \
+    hipError_t e_ = (expr);                                                          \
+    if (e_ != hipSuccess) return fail(LLE_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+static double wbytes(const WeightDev& w) { return (double)w.bytes; }
+
+// BertModel.Forward (internal/embed/bert.go:216-285) for B right-padded rows of length L,
+// followed (when out != nullptr) by MeanPool + L2Normalize (+ Matryoshka).
+// ids / mask / out are device pointers already placed in m's workspace or the caller's.
+static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim, float* d_out,
+                   hipStream_t st) {
+  const int D = m->D, H = m->H, F = m->F;
+  const int T = B * L, Lp = (L + 63) / 64 * 64;
+  {
+    EmbedArgs a{d_ids, T, m->vocab, m->tok_type, m->tok, m->tok_row_bytes, m->type0, m->enw, m->enb, m->eps, D,
+                m->h, m->h16, m->status};
+    Scope s(m, st, "embed_ln", 0, (double)T * (m->tok_row_bytes + D * 6));
+    LAUNCH(launch_embed_ln(a, st));
+  }
+  {
+    Scope s(m, st, "kv_range", 0, (double)T * 4);
+    LAUNCH(launch_kv_range(d_mask, B, L, m->kv_range, st));
+  }
+  for (int l = 0; l < m->n_layer; l++) {
+    Layer& ly = m->layers[l];
+    GemmArgs g{};
+    g.M = T;
+    g.rope_cos = m->rope_cos;
+    g.rope_sin = m->rope_sin;
+    g.L = L;
+    g.Lp = Lp;
+    g.n_head = H;
+    g.d_model = D;
+    g.part = m->part;
+    {
+      g.w = &ly.qkv;
+      g.x = m->h16;
+      g.q = m->q;
+      g.k = m->k;
+      g.vt = m->vt;
+      Scope s(m, st, "gemm_qkv", 2.0 * T * ly.qkv.N * ly.qkv.K, wbytes(ly.qkv) + (double)T * (D * 2 + 3 * D * 2));
+      LAUNCH(launch_gemm(g, EPI_QKV, st));
+    }
+    {
+      AttnArgs a{m->q, m->k, m->vt, d_mask, m->kv_range, m->attn, B, L, Lp, H, D};
+      Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
+      LAUNCH(launch_attention(a, st));
+    }
+    {
+      g.w = &ly.out;
+      g.x = m->attn;
+      g.y = m->h;
+      Scope s(m, st, "gemm_out", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 8));
+      LAUNCH(launch_gemm(g, EPI_RESID, st));
+    }
+    {
+      Scope s(m, st, "ln", 0, (double)T * D * 10);
+      LAUNCH(launch_ln(m->h, m->h16, ly.anw, ly.anb, m->eps, T, D, st));
+    }
+    {
+      g.w = &ly.upgate;
+      g.x = m->h16;
+      g.g = m->ff;
+      Scope s(m, st, "gemm_upgate", 2.0 * T * ly.upgate.N * ly.upgate.K, wbytes(ly.upgate) + (double)T * (D * 2 + F * 2));
+      LAUNCH(launch_gemm(g, EPI_GEGLU, st));
+    }
+    {
+      g.w = &ly.down;
+      g.x = m->ff;
+      g.y = m->h;
+      Scope s(m, st, "gemm_down", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 8));
+      LAUNCH(launch_gemm(g, EPI_RESID, st));
+    }
+    {
+      Scope s(m, st, "ln", 0, (double)T * D * 10);
+      LAUNCH(launch_ln(m->h, m->h16, ly.onw, ly.onb, m->eps, T, D, st));
+    }
+  }
+  if (d_out) {
+    Scope s(m, st, "pool", 0, (double)T * D * 4);
+    LAUNCH(launch_pool(m->h, d_mask, B, L, D, out_dim, d_out, st));
+  }
+  return LLE_OK;
+}
+
+static int check_batch(lle_model* m, int B, int L) {
+  if (!m) return fail(LLE_EINVAL, "null model");
+  if (B <= 0 || L <= 0) return fail(LLE_EINVAL, "B and L must be positive");
+  if (L > m->max_seq)
+    return fail(LLE_EINVAL, "sequence length " + std::to_string(L) + " exceeds context_length " + std::to_string(m->max_seq));
+  if ((int64_t)B * L > (int64_t)1 << 26) return fail(LLE_EINVAL, "batch too large");
+  return LLE_OK;
+}
+
+static int check_ids(lle_model* m, const int32_t* ids, int64_t n) {
+  for (int64_t i = 0; i < n; i++)
+    if (ids[i] < 0 || ids[i] >= m->vocab)
+      return fail(LLE_EINVAL, "token embedding " + std::to_string(ids[i]) + ": id out of range [0, " + std::to_string(m->vocab) + ")");
+  return LLE_OK;
+}
+
+// Host-pointer batch: H2D, forward, D2H, sync.
+static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B, int L, int out_dim, float* out,
+                    float* hidden) {
+  int rc = check_batch(m, B, L);
+  if (rc) return rc;
+  if (!ids || (!out && !hidden)) return fail(LLE_EINVAL, "null pointer");
+  if ((rc = check_ids(m, ids, (int64_t)B * L))) return rc;
+  std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  if ((rc = ensure_ws(m, B, L))) return rc;
+  const size_t T = (size_t)B * L;
+  hipStream_t st = m->stream;
+  LLE_HIP(hipMemcpyAsync(m->ids, ids, T * 4, hipMemcpyHostToDevice, st));
+  if (mask) {
+    LLE_HIP(hipMemcpyAsync(m->mask, mask, T * 4, hipMemcpyHostToDevice, st));
+  } else {
+    std::vector<int32_t> ones(T, 1);
+    LLE_HIP(hipMemcpyAsync(m->mask, ones.data(), T * 4, hipMemcpyHostToDevice, st));
+    LLE_HIP(hipStreamSynchronize(st));
+  }
+  LLE_HIP(hipMemsetAsync(m->status, 0, 4, st));
+  if ((rc = forward(m, m->ids, m->mask, B, L, out_dim, out ? m->out : nullptr, st))) return rc;
+  const int od = std::min(out_dim, m->D);
+  if (out) LLE_HIP(hipMemcpyAsync(out, m->out, (size_t)B * od * 4, hipMemcpyDeviceToHost, st));
+  if (hidden) LLE_HIP(hipMemcpyAsync(hidden, m->h, T * m->D * 4, hipMemcpyDeviceToHost, st));
+  LLE_HIP(hipStreamSynchronize(st));
+  if (m->timing) collect_timing(m);
+  return LLE_OK;
+}
+
+// Upload one projection: GGUF bytes of an [N][K] matrix -> re-laid-out planes in HBM.
+static int upload_weight(int device, int type, const uint8_t* gguf, int K, int N, WeightDev* wd, std::vector<void*>* allocs) {
+  if (type == 15 || type == 16) type = LLE_TYPE_Q5_K;  // DequantWeightMatrix maps 13,15,16 to Q5_K (gemm.go:241)
+  if (!(type == 0 || type == 8 || type == 12 || type == 13 || type == 14))
+    return fail(LLE_EUNSUPPORTED, "unsupported projection weight type " + std::to_string(type));
+  if (K % 256 != 0 || N % 128 != 0)
+    return fail(LLE_EUNSUPPORTED, "projection shape K=" + std::to_string(K) + " N=" + std::to_string(N) +
+                                      " (need K % 256 == 0, N % 128 == 0)");
+  size_t off[4], total;
+  plane_offsets(type, K, N, off, &total);
+  std::vector<uint8_t> host(total, 0);
+  repack_rows(type, gguf, K, N, host.data(), off);
+  void* d = nullptr;
+  hipError_t e = hipMalloc(&d, total);
+  if (e != hipSuccess) return fail(LLE_ENOMEM, std::string("weight hipMalloc: ") + hipGetErrorString(e));
+  if (allocs) allocs->push_back(d);
+  LLE_HIP(hipMemcpy(d, host.data(), total, hipMemcpyHostToDevice));
+  wd->type = type;
+  wd->K = K;
+  wd->N = N;
+  wd->base = d;
+  wd->bytes = weight_dev_bytes(type, K, N);
+  uint8_t* b = (uint8_t*)d;
+  wd->p0 = b + off[0];
+  wd->p1 = b + off[1];
+  wd->p2 = b + off[2];
+  wd->p3 = b + off[3];
+  (void)device;
+  return LLE_OK;
+}
+
+static int check_tensor(const lle_tensor& t, const char* name, int64_t ne0, int64_t ne1) {
+  if (!t.data) return fail(LLE_ENOTFOUND, std::string("tensor \"") + name + "\" not found");
+  if (t.ne0 != ne0 || (ne1 >= 0 && t.ne1 != ne1))
+    return fail(LLE_EINVAL, std::string(name) + ": shape [" + std::to_string(t.ne0) + ", " + std::to_string(t.ne1) +
+                                "], expected [" + std::to_string(ne0) + ", " + std::to_string(ne1) + "]");
+  const int64_t rb = row_bytes(t.type, t.ne0);
+  if (rb < 0) return fail(LLE_EUNSUPPORTED, std::string(name) + ": unsupported ggml type " + std::to_string(t.type));
+  if (t.nbytes < rb * std::max<int64_t>(t.ne1, 1))
+    return fail(LLE_EINVAL, std::string(name) + ": data shorter than its ByteSize");
+  return LLE_OK;
+}
+
+// Tensor.Dequantize of a small vector on the device (tensor.go:51-66 accepts 0/8/12/13/14).
+static int upload_vec(lle_model* m, const lle_tensor& t, int n, float** out) {
+  if (!(t.type == 0 || t.type == 8 || t.type == 12 || t.type == 13 || t.type == 14))
+    return fail(LLE_EUNSUPPORTED, "ggml: dequantize not implemented for type " + std::to_string(t.type));
+  const int64_t rb = row_bytes(t.type, n);
+  void* raw = nullptr;
+  int rc = dev_alloc(m, &raw, (size_t)rb);
+  if (rc) return rc;
+  LLE_HIP(hipMemcpy(raw, t.data, (size_t)rb, hipMemcpyHostToDevice));
+  void* f = nullptr;
+  if ((rc = dev_alloc(m, &f, (size_t)n * 4))) return rc;
+  LAUNCH(launch_dequant_raw(t.type, (const uint8_t*)raw, n, (float*)f, m->stream));
+  LLE_HIP(hipStreamSynchronize(m->stream));
+  *out = (float*)f;
+  return LLE_OK;
+}
+
+static void destroy_model(lle_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->device);
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  ws_free(m);
+  for (void* p : m->allocs) (void)hipFree(p);
+  for (auto& t : m->pending) {
+    (void)hipEventDestroy(t.a);
+    (void)hipEventDestroy(t.b);
+  }
+  for (auto e : m->event_pool) (void)hipEventDestroy(e);
+  if (m->status) (void)hipFree(m->status);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+static int create_model(const lle_model_desc* d, lle_model** out) {
+  if (!d || !out) return fail(LLE_EINVAL, "null argument");
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (d->n_layer <= 0 || d->d_model <= 0) return fail(LLE_EINVAL, "embed: missing model params in GGUF metadata");
+  if (d->n_head <= 0 || d->d_model % d->n_head != 0 || d->d_model / d->n_head != 64)
+    return fail(LLE_EUNSUPPORTED, "head_dim must be 64 (d_model=" + std::to_string(d->d_model) + ", heads=" +
+                                      std::to_string(d->n_head) + ")");
+  if (d->d_model % 256 != 0 || d->d_model > 1024)
+    return fail(LLE_EUNSUPPORTED, "d_model must be a multiple of 256 and <= 1024");
+  if (d->d_ff <= 0 || d->d_ff % 256 != 0) return fail(LLE_EUNSUPPORTED, "feed_forward_length must be a multiple of 256");
+  if (d->max_seq <= 0) return fail(LLE_EINVAL, "context_length must be positive");
+  const int D = d->d_model, F = d->d_ff;
+  if ((rc = check_tensor(d->token_embd, "token_embd.weight", D, -1))) return rc;
+  if (!(d->token_embd.type == 0 || d->token_embd.type == 8 || d->token_embd.type == 12 || d->token_embd.type == 13 ||
+        d->token_embd.type == 14))
+    return fail(LLE_EUNSUPPORTED, "unsupported embedding type: " + std::to_string(d->token_embd.type));
+  if ((rc = check_tensor(d->token_types, "token_types.weight", D, -1))) return rc;
+  if ((rc = check_tensor(d->embd_norm_w, "token_embd_norm.weight", D, -1))) return rc;
+  if ((rc = check_tensor(d->embd_norm_b, "token_embd_norm.bias", D, -1))) return rc;
+  if (!d->qkv || !d->out || !d->up || !d->gate || !d->down || !d->attn_norm_w || !d->attn_norm_b || !d->out_norm_w ||
+      !d->out_norm_b)
+    return fail(LLE_EINVAL, "null layer tensor array");
+  for (int l = 0; l < d->n_layer; l++) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    if ((rc = check_tensor(d->qkv[l], (p + "attn_qkv.weight").c_str(), D, 3 * D))) return rc;
+    if ((rc = check_tensor(d->out[l], (p + "attn_output.weight").c_str(), D, D))) return rc;
+    if ((rc = check_tensor(d->up[l], (p + "ffn_up.weight").c_str(), D, F))) return rc;
+    if ((rc = check_tensor(d->gate[l], (p + "ffn_gate.weight").c_str(), D, F))) return rc;
+    if ((rc = check_tensor(d->down[l], (p + "ffn_down.weight").c_str(), F, D))) return rc;
+    if ((rc = check_tensor(d->attn_norm_w[l], (p + "attn_output_norm.weight").c_str(), D, -1))) return rc;
+    if ((rc = check_tensor(d->attn_norm_b[l], (p + "attn_output_norm.bias").c_str(), D, -1))) return rc;
+    if ((rc = check_tensor(d->out_norm_w[l], (p + "layer_output_norm.weight").c_str(), D, -1))) return rc;
+    if ((rc = check_tensor(d->out_norm_b[l], (p + "layer_output_norm.bias").c_str(), D, -1))) return rc;
+    const int tu = d->up[l].type == 15 || d->up[l].type == 16 ? 13 : d->up[l].type;
+    const int tg = d->gate[l].type == 15 || d->gate[l].type == 16 ? 13 : d->gate[l].type;
+    if (tu != tg)
+      return fail(LLE_EUNSUPPORTED, p + "ffn_up and ffn_gate have different ggml types; the fused up||gate GEMM needs one");
+  }
+
+  lle_model* m = new lle_model();
+  m->device = g_device;
+  m->n_layer = d->n_layer;
+  m->D = D;
+  m->H = d->n_head;
+  m->F = F;
+  m->max_seq = d->max_seq;
+  m->vocab = (int)d->token_embd.ne1;
+  memcpy(&m->eps, &d->ln_eps_bits, 4);
+  memcpy(&m->rope_base, &d->rope_base_bits, 4);
+  auto bail = [&](int code) {
+    destroy_model(m);
+    return code;
+  };
+  if (hipSetDevice(m->device) != hipSuccess) return bail(fail(LLE_EDEVICE, "hipSetDevice failed"));
+  if (hipStreamCreate(&m->stream) != hipSuccess) return bail(fail(LLE_EDEVICE, "hipStreamCreate failed"));
+  if (hipMalloc((void**)&m->status, 4) != hipSuccess) return bail(fail(LLE_ENOMEM, "hipMalloc status"));
+  (void)hipMemset(m->status, 0, 4);
+
+  // token_embd stays in its GGUF layout: rows are gathered, not streamed.
+  m->tok_type = d->token_embd.type;
+  m->tok_row_bytes = row_bytes(m->tok_type, D);
+  const size_t tok_bytes = (size_t)m->tok_row_bytes * m->vocab;
+  void* p = nullptr;
+  if ((rc = dev_alloc(m, &p, tok_bytes))) return bail(rc);
+  if (hipMemcpy(p, d->token_embd.data, tok_bytes, hipMemcpyHostToDevice) != hipSuccess)
+    return bail(fail(LLE_EDEVICE, "upload token_embd"));
+  m->tok = (uint8_t*)p;
+  // getEmbedding(TokenTypes, 0): row 0 of token_types
+  {
+    lle_tensor t0 = d->token_types;
+    t0.ne1 = 1;
+    if ((rc = upload_vec(m, t0, D, &m->type0))) return bail(rc);
+  }
+  if ((rc = upload_vec(m, d->embd_norm_w, D, &m->enw))) return bail(rc);
+  if ((rc = upload_vec(m, d->embd_norm_b, D, &m->enb))) return bail(rc);
+
+  m->layers.resize(m->n_layer);
+  for (int l = 0; l < m->n_layer; l++) {
+    Layer& ly = m->layers[l];
+    if ((rc = upload_weight(m->device, d->qkv[l].type, (const uint8_t*)d->qkv[l].data, D, 3 * D, &ly.qkv, &m->allocs)))
+      return bail(rc);
+    if ((rc = upload_weight(m->device, d->out[l].type, (const uint8_t*)d->out[l].data, D, D, &ly.out, &m->allocs)))
+      return bail(rc);
+    // up || gate, rows interleaved: fused row 2q = up row q, 2q+1 = gate row q
+    {
+      const int64_t rb = row_bytes(d->up[l].type, D);
+      std::vector<uint8_t> fused((size_t)rb * 2 * F);
+      const uint8_t* up = (const uint8_t*)d->up[l].data;
+      const uint8_t* gt = (const uint8_t*)d->gate[l].data;
+      for (int qrow = 0; qrow < F; qrow++) {
+        memcpy(fused.data() + (size_t)(2 * qrow) * rb, up + (size_t)qrow * rb, rb);
+        memcpy(fused.data() + (size_t)(2 * qrow + 1) * rb, gt + (size_t)qrow * rb, rb);
+      }
+      if ((rc = upload_weight(m->device, d->up[l].type, fused.data(), D, 2 * F, &ly.upgate, &m->allocs))) return bail(rc);
+    }
+    if ((rc = upload_weight(m->device, d->down[l].type, (const uint8_t*)d->down[l].data, F, D, &ly.down, &m->allocs)))
+      return bail(rc);
+    if ((rc = upload_vec(m, d->attn_norm_w[l], D, &ly.anw))) return bail(rc);
+    if ((rc = upload_vec(m, d->attn_norm_b[l], D, &ly.anb))) return bail(rc);
+    if ((rc = upload_vec(m, d->out_norm_w[l], D, &ly.onw))) return bail(rc);
+    if ((rc = upload_vec(m, d->out_norm_b[l], D, &ly.onb))) return bail(rc);
+  }
+
+  // NewRoPETable (internal/ggml/ops_simd.go:107-124): f32 frequency, f32 angle, f64 cos/sin.
+  {
+    const int nrot = 32;
+    std::vector<float> c((size_t)m->max_seq * nrot), s((size_t)m->max_seq * nrot);
+    for (int pos = 0; pos < m->max_seq; pos++)
+      for (int i = 0; i < nrot; i++) {
+        const float freq = 1.0f / (float)pow((double)m->rope_base, (double)(2 * i) / 64.0);
+        const float theta = freq * (float)pos;
+        c[(size_t)pos * nrot + i] = (float)cos((double)theta);
+        s[(size_t)pos * nrot + i] = (float)sin((double)theta);
+      }
+    void *dc = nullptr, *ds = nullptr;
+    if ((rc = dev_alloc(m, &dc, c.size() * 4))) return bail(rc);
+    if ((rc = dev_alloc(m, &ds, s.size() * 4))) return bail(rc);
+    if (hipMemcpy(dc, c.data(), c.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ds, s.data(), s.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bail(fail(LLE_EDEVICE, "upload rope table"));
+    m->rope_cos = (float*)dc;
+    m->rope_sin = (float*)ds;
+  }
+  *out = m;
+  return LLE_OK;
+}
+
+}  // namespace lle
+
+using namespace lle;
+
+extern "C" {
+
+int32_t lle_abi_version(void) { return LLE_ABI_VERSION; }
+
+const char* lle_last_error(void) { return g_err.c_str(); }
+
+int32_t lle_init(int32_t device) {
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) return fail(LLE_EDEVICE, "no HIP device available");
+  if (device < 0 || device >= n) return fail(LLE_EINVAL, "device ordinal out of range");
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail(LLE_EDEVICE, std::string("hipGetDeviceProperties: ") + hipGetErrorString(e));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(LLE_EDEVICE, std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950");
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return fail(LLE_EDEVICE, std::string("hipSetDevice: ") + hipGetErrorString(e));
+  g_device = device;
+  return LLE_OK;
+}
+
+int32_t lle_info(char* buf, int32_t cap) {
+  if (!buf || cap <= 0) return fail(LLE_EINVAL, "null buffer");
+  std::string s = "llmembed-hip abi=" + std::to_string(LLE_ABI_VERSION) + " arch=gfx950";
+  if (g_device >= 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, g_device) == hipSuccess)
+      s += std::string(" device=") + std::to_string(g_device) + " name=" + prop.name + " cus=" +
+           std::to_string(prop.multiProcessorCount) + " hbm_gib=" + std::to_string(prop.totalGlobalMem >> 30);
+  } else {
+    s += " device=uninitialised";
+  }
+  s += " gemm=mfma_f32_16x16x32_f16(dequant->f16 in LDS, f32 accumulate, 256-wide K chunks)";
+  s += " attention=mfma flash (online max, exact x<-10 cutoff)";
+  snprintf(buf, (size_t)cap, "%s", s.c_str());
+  return (int32_t)std::min<size_t>(s.size(), (size_t)cap - 1);
+}
+
+int32_t lle_f16_to_f32(const uint16_t* h, int64_t n, float* out) {
+  if (!h || !out || n < 0) return fail(LLE_EINVAL, "bad argument");
+  int rc = ensure_init();
+  if (rc) return rc;
+  LLE_HIP(hipSetDevice(g_device));
+  void *dh = nullptr, *df = nullptr;
+  LLE_HIP(hipMalloc(&dh, (size_t)std::max<int64_t>(n, 1) * 2));
+  hipError_t e = hipMalloc(&df, (size_t)std::max<int64_t>(n, 1) * 4);
+  if (e != hipSuccess) {
+    (void)hipFree(dh);
+    return fail(LLE_ENOMEM, "hipMalloc");
+  }
+  e = hipMemcpy(dh, h, (size_t)n * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_f16_to_f32_bits((const uint16_t*)dh, (float*)df, n, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(out, df, (size_t)n * 4, hipMemcpyDeviceToHost);
+  (void)hipFree(dh);
+  (void)hipFree(df);
+  if (e != hipSuccess) return fail(LLE_EDEVICE, std::string("f16 decode: ") + hipGetErrorString(e));
+  return LLE_OK;
+}
+
+int32_t lle_dequant(int32_t type, const void* blocks, int64_t n, float* out) {
+  if (!blocks || !out || n < 0) return fail(LLE_EINVAL, "bad argument");
+  if (type == 15 || type == 16) type = LLE_TYPE_Q5_K;
+  const int64_t bs = type == 0 ? 1 : type == 8 ? 32 : 256;
+  const int64_t rb = row_bytes(type, n);
+  if (rb < 0) return fail(LLE_EUNSUPPORTED, "ggml: dequantize not implemented for type " + std::to_string(type));
+  if (n % bs) return fail(LLE_EINVAL, "element count must be a whole number of blocks");
+  int rc = ensure_init();
+  if (rc) return rc;
+  LLE_HIP(hipSetDevice(g_device));
+  void *db = nullptr, *df = nullptr;
+  LLE_HIP(hipMalloc(&db, (size_t)std::max<int64_t>(rb, 1)));
+  hipError_t e = hipMalloc(&df, (size_t)std::max<int64_t>(n, 1) * 4);
+  if (e != hipSuccess) {
+    (void)hipFree(db);
+    return fail(LLE_ENOMEM, "hipMalloc");
+  }
+  e = hipMemcpy(db, blocks, (size_t)rb, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_dequant_raw(type, (const uint8_t*)db, n, (float*)df, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(out, df, (size_t)n * 4, hipMemcpyDeviceToHost);
+  (void)hipFree(db);
+  (void)hipFree(df);
+  if (e != hipSuccess) return fail(LLE_EDEVICE, std::string("dequant: ") + hipGetErrorString(e));
+  return LLE_OK;
+}
+
+int32_t lle_model_create(const lle_model_desc* d, lle_model** out) { return create_model(d, out); }
+
+int32_t lle_model_destroy(lle_model* m) {
+  if (!m) return fail(LLE_EINVAL, "null model");
+  destroy_model(m);
+  return LLE_OK;
+}
+
+int32_t lle_model_dims(const lle_model* m, int32_t* dims) {
+  if (!m || !dims) return fail(LLE_EINVAL, "null argument");
+  dims[0] = m->n_layer;
+  dims[1] = m->D;
+  dims[2] = m->H;
+  dims[3] = m->F;
+  dims[4] = m->max_seq;
+  dims[5] = m->vocab;
+  return LLE_OK;
+}
+
+int32_t lle_embed(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t L, int32_t out_dim, float* out) {
+  if (out_dim < 1) out_dim = 1;  // SetTargetDim clamps (embedder.go:142-150)
+  return run_host(m, ids, mask, 1, L, out_dim, out, nullptr);
+}
+
+int32_t lle_embed_batch(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L, int32_t out_dim,
+                        float* out) {
+  if (out_dim < 1) out_dim = 1;
+  return run_host(m, ids, mask, B, L, out_dim, out, nullptr);
+}
+
+int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L, float* hidden) {
+  return run_host(m, ids, mask, B, L, m ? m->D : 0, nullptr, hidden);
+}
+
+int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int32_t B, int32_t L,
+                              int32_t out_dim, float* d_out, void* stream) {
+  int rc = check_batch(m, B, L);
+  if (rc) return rc;
+  if (!d_ids || !d_mask || !d_out) return fail(LLE_EINVAL, "null device pointer");
+  if (out_dim < 1) out_dim = 1;
+  std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  if ((rc = ensure_ws(m, B, L))) return rc;
+  hipStream_t st = stream ? (hipStream_t)stream : m->stream;
+  if ((rc = forward(m, d_ids, d_mask, B, L, out_dim, d_out, st))) return rc;
+  if (m->timing) {
+    LLE_HIP(hipStreamSynchronize(st));
+    collect_timing(m);
+  }
+  return LLE_OK;
+}
+
+int32_t lle_model_status(lle_model* m, int32_t* status) {
+  if (!m || !status) return fail(LLE_EINVAL, "null argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  LLE_HIP(hipDeviceSynchronize());
+  LLE_HIP(hipMemcpy(status, m->status, 4, hipMemcpyDeviceToHost));
+  return LLE_OK;
+}
+
+int32_t lle_model_set_timing(lle_model* m, int32_t enable) {
+  if (!m) return fail(LLE_EINVAL, "null model");
+  std::lock_guard<std::mutex> lk(m->mu);
+  m->timing = enable != 0;
+  m->totals.clear();
+  return LLE_OK;
+}
+
+int32_t lle_model_get_timing(lle_model* m, lle_kernel_time* out, int32_t cap, int32_t* n_out) {
+  if (!m || !n_out) return fail(LLE_EINVAL, "null argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  const int n = (int)m->totals.size();
+  for (int i = 0; i < n && i < cap && out; i++) out[i] = m->totals[i];
+  *n_out = n;
+  return LLE_OK;
+}
+
+int32_t lle_weight_create(int32_t type, const void* blocks, int32_t K, int32_t N, lle_weight** out) {
+  if (!blocks || !out || K <= 0 || N <= 0) return fail(LLE_EINVAL, "bad argument");
+  int rc = ensure_init();
+  if (rc) return rc;
+  LLE_HIP(hipSetDevice(g_device));
+  lle_weight* w = new lle_weight();
+  w->device = g_device;
+  if ((rc = upload_weight(g_device, type, (const uint8_t*)blocks, K, N, &w->w, nullptr))) {
+    delete w;
+    return rc;
+  }
+  if (hipStreamCreate(&w->stream) != hipSuccess) {
+    (void)hipFree(w->w.base);
+    delete w;
+    return fail(LLE_EDEVICE, "hipStreamCreate");
+  }
+  *out = w;
+  return LLE_OK;
+}
+
+int32_t lle_weight_destroy(lle_weight* w) {
+  if (!w) return fail(LLE_EINVAL, "null weight");
+  (void)hipSetDevice(w->device);
+  (void)hipStreamSynchronize(w->stream);
+  (void)hipFree(w->w.base);
+  (void)hipStreamDestroy(w->stream);
+  delete w;
+  return LLE_OK;
+}
+
+int32_t lle_weight_dequant(const lle_weight* w, float* out) {
+  if (!w || !out) return fail(LLE_EINVAL, "null argument");
+  LLE_HIP(hipSetDevice(w->device));
+  void* d = nullptr;
+  const size_t n = (size_t)w->w.K * w->w.N;
+  LLE_HIP(hipMalloc(&d, n * 4));
+  hipError_t e = launch_dequant_weight(w->w, (float*)d, w->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+  if (e == hipSuccess) e = hipMemcpy(out, d, n * 4, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(LLE_EDEVICE, std::string("weight dequant: ") + hipGetErrorString(e));
+  return LLE_OK;
+}
+
+static int gemm_enqueue(const lle_weight* w, const float* dX, void* dx16, int M, float* dY, float* part, hipStream_t st) {
+  LAUNCH(launch_f32_to_f16(dX, (__half*)dx16, (int64_t)M * w->w.K, st));
+  GemmArgs g{};
+  g.w = &w->w;
+  g.x = (const __half*)dx16;
+  g.M = M;
+  g.y = dY;
+  g.part = part;
+  LAUNCH(launch_gemm(g, EPI_F32, st));
+  return LLE_OK;
+}
+
+int32_t lle_gemm_async(const lle_weight* w, const float* d_X, void* d_x16, int32_t M, float* d_Y, void* stream) {
+  if (!w || !d_X || !d_x16 || !d_Y || M <= 0) return fail(LLE_EINVAL, "bad argument");
+  if (M <= 64) return fail(LLE_EINVAL, "lle_gemm_async needs M > 64 (small M uses a split-K workspace: use lle_gemm)");
+  LLE_HIP(hipSetDevice(w->device));
+  return gemm_enqueue(w, d_X, d_x16, M, d_Y, nullptr, stream ? (hipStream_t)stream : w->stream);
+}
+
+int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y) {
+  if (!w || !X || !Y || M <= 0) return fail(LLE_EINVAL, "bad argument");
+  LLE_HIP(hipSetDevice(w->device));
+  const size_t K = (size_t)w->w.K, N = (size_t)w->w.N;
+  void *dX = nullptr, *dx16 = nullptr, *dY = nullptr, *dP = nullptr;
+  hipError_t e = hipMalloc(&dX, M * K * 4);
+  if (e == hipSuccess) e = hipMalloc(&dx16, M * K * 2);
+  if (e == hipSuccess) e = hipMalloc(&dY, M * N * 4);
+  if (e == hipSuccess && M <= 64) e = hipMalloc(&dP, (K / 256) * (size_t)M * N * 4);
+  int rc = LLE_OK;
+  if (e != hipSuccess) rc = fail(LLE_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+  if (!rc && hipMemcpy(dX, X, M * K * 4, hipMemcpyHostToDevice) != hipSuccess) rc = fail(LLE_EDEVICE, "copy X");
+  if (!rc) rc = gemm_enqueue(w, (const float*)dX, dx16, M, (float*)dY, (float*)dP, w->stream);
+  if (!rc && hipStreamSynchronize(w->stream) != hipSuccess) rc = fail(LLE_EDEVICE, "gemm sync");
+  if (!rc && hipMemcpy(Y, dY, M * N * 4, hipMemcpyDeviceToHost) != hipSuccess) rc = fail(LLE_EDEVICE, "copy Y");
+  (void)hipFree(dX);
+  (void)hipFree(dx16);
+  (void)hipFree(dY);
+  if (dP) (void)hipFree(dP);
+  return rc;
+}
+
+}  // extern "C"

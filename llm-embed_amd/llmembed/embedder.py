@@ -1,0 +1,138 @@
+"""Host-side mirror of the reference's embed API over the HIP C ABI.
+
+Reference: internal/embed/embedder.go
+  Embedder{model, tokenizer, targetDim, TaskPrefix}    :11-16
+  Load(modelPath)                                        :19-42
+  (*Embedder).Embed(text)                                :46-71
+  (*Embedder).EmbedBatch(texts)                          :75-133
+  Dim / SetTargetDim / Model                             :136-153
+Tokenisation (internal/embed/tokenizer.go) is host string work outside this path, so Embed and
+EmbedBatch take token ids (what Encode returns: [CLS] ... [SEP], mask all ones). EmbedBatch is
+truly batched: one padded [B][L] forward on the GPU, each row bit-identical to Embed of that row.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import LLEError, check, ptr
+
+
+class BertModel:
+    """Device-resident nomic-bert model (BertModel + PreDequant, internal/embed/bert.go:14-87,542-576)."""
+
+    def __init__(self, handle: C.c_void_p):
+        self.h = handle
+        dims = np.zeros(6, np.int32)
+        check(_lib.lib().lle_model_dims(self.h, ptr(dims)))
+        (self.num_layers, self.hidden_dim, self.num_heads, self.ffn_dim, self.max_seq_len,
+         self.vocab_size) = (int(x) for x in dims)
+        self.head_dim = self.hidden_dim // self.num_heads
+
+    @classmethod
+    def load(cls, path: str) -> "BertModel":
+        """LoadBertModel (bert.go:91-212) + upload."""
+        h = C.c_void_p()
+        check(_lib.lib().lle_model_load_gguf(path.encode(), C.byref(h)))
+        return cls(h)
+
+    def forward(self, ids, mask=None) -> np.ndarray:
+        """Forward (bert.go:216-285): hidden states [L][hidden_dim] of one sequence, or
+        [B][L][hidden_dim] of a padded batch."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        single = ids.ndim == 1
+        ids2 = ids[None, :] if single else ids
+        mask2 = np.ones_like(ids2) if mask is None else np.ascontiguousarray(mask, np.int32).reshape(ids2.shape)
+        B, L = ids2.shape
+        out = np.empty((B, L, self.hidden_dim), np.float32)
+        check(_lib.lib().lle_forward_hidden(self.h, ptr(ids2), ptr(mask2), B, L, ptr(out)))
+        return out[0] if single else out
+
+    def set_timing(self, on: bool):
+        check(_lib.lib().lle_model_set_timing(self.h, 1 if on else 0))
+
+    def timing(self) -> dict:
+        n = C.c_int32()
+        arr = (_lib.KernelTime * 64)()
+        check(_lib.lib().lle_model_get_timing(self.h, arr, 64, C.byref(n)))
+        return {arr[i].name.decode(): dict(launches=arr[i].launches, total_ms=arr[i].total_ms,
+                                           flops=arr[i].flops, bytes=arr[i].bytes)
+                for i in range(min(n.value, 64))}
+
+    def close(self):
+        if getattr(self, "h", None):
+            _lib.lib().lle_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Embedder:
+    """Public embedding API (embedder.go:11-16)."""
+
+    def __init__(self, model: BertModel):
+        self._model = model
+        self.target_dim = model.hidden_dim
+        self.task_prefix = "search_query: "  # embedder.go:40; applies to text, kept for API parity
+
+    @classmethod
+    def load(cls, model_path: str) -> "Embedder":
+        try:
+            m = BertModel.load(model_path)
+        except LLEError as e:
+            raise LLEError(e.code, f"embed: load model: {e}") from None
+        return cls(m)
+
+    def embed(self, ids, mask=None) -> np.ndarray:
+        """Embed (embedder.go:46-71): forward + MeanPool + L2Normalize (+ Matryoshka)."""
+        ids = np.ascontiguousarray(ids, np.int32).reshape(-1)
+        mask = np.ones_like(ids) if mask is None else np.ascontiguousarray(mask, np.int32).reshape(-1)
+        out = np.empty(min(self.target_dim, self._model.hidden_dim), np.float32)
+        rc = _lib.lib().lle_embed(self._model.h, ptr(ids), ptr(mask), ids.size, self.target_dim, ptr(out))
+        if rc:
+            raise LLEError(rc, f"embed: forward: {_lib.lib().lle_last_error().decode()}")
+        return out
+
+    def embed_batch(self, seqs) -> list | None:
+        """EmbedBatch (embedder.go:75-133) as one padded batched forward. `seqs` is a list of
+        token-id sequences; returns a list of vectors in input order."""
+        n = len(seqs)
+        if n == 0:
+            return None
+        if n == 1:
+            return [self.embed(seqs[0])]
+        lens = [len(s) for s in seqs]
+        L = max(lens)
+        ids = np.zeros((n, L), np.int32)
+        mask = np.zeros((n, L), np.int32)
+        for i, s in enumerate(seqs):
+            ids[i, :lens[i]] = s
+            mask[i, :lens[i]] = 1
+        return list(self.embed_padded(ids, mask))
+
+    def embed_padded(self, ids, mask) -> np.ndarray:
+        """Batched embed of a right-padded [B][L] id matrix with its attention mask."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        mask = np.ascontiguousarray(mask, np.int32)
+        B, L = ids.shape
+        out = np.empty((B, min(self.target_dim, self._model.hidden_dim)), np.float32)
+        rc = _lib.lib().lle_embed_batch(self._model.h, ptr(ids), ptr(mask), B, L, self.target_dim, ptr(out))
+        if rc:
+            raise LLEError(rc, f"embed: batch: {_lib.lib().lle_last_error().decode()}")
+        return out
+
+    def dim(self) -> int:
+        return self.target_dim
+
+    def set_target_dim(self, dim: int):
+        """SetTargetDim (embedder.go:142-150): clamp to [1, hidden_dim]."""
+        self.target_dim = max(1, min(int(dim), self._model.hidden_dim))
+
+    def model(self) -> BertModel:
+        return self._model

@@ -1,0 +1,155 @@
+"""GPU parity of the building blocks, through the C ABI: f16 decode, dequantisation (raw GGUF
+layout and the GEMM's own re-laid-out planes), and the quantised projection GEMM (config 2).
+
+Bars: bit-exact for f16 decode and dequantisation; GEMM outputs within a tolerance set by the
+f16 rounding of X and W (each relative 2^-11 at most, 2^-12 rms), stated per test.
+"""
+import numpy as np
+import pytest
+
+import kat
+import oracle
+from llmembed import quant
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [quant.Q8_0, quant.Q4_K, quant.Q5_K, quant.Q6_K, quant.F32]
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def test_f16_decode_exhaustive(gpu):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    assert np.array_equal(bits(gpu.f16_to_f32(h)), bits(oracle.f16_to_f32(h)))
+
+
+@pytest.mark.parametrize("t", FORMATS)
+def test_dequant_raw_bitexact(gpu, t):
+    rng = np.random.default_rng(100 + t)
+    w = (rng.standard_normal((24, 768)) * 0.02).astype(np.float32)
+    blocks = quant.quantize(t, w, rng).reshape(-1)
+    got = gpu.dequant(t, blocks, w.size)
+    assert np.array_equal(bits(got), bits(oracle.dequant(t, blocks, w.size)))
+
+
+def test_dequant_raw_kats(gpu):
+    for _, blk, x, expected in kat.q8_0_cases():
+        v = gpu.dequant(quant.Q8_0, blk, 32)
+        assert float(np.dot(v.astype(np.float64), x)) == expected
+    for _, blk, expected in kat.q5k_cases():
+        assert np.array_equal(gpu.dequant(quant.Q5_K, blk, 256), expected)
+    v = gpu.dequant(quant.Q5_K, kat.q5k_highbit_only_block(), 256)
+    assert float(v[96:128].sum()) == 512.0
+    v = gpu.dequant(quant.Q6_K, kat.q6k_known_scales(), 256)
+    assert float(v.astype(np.float64).sum()) == kat.Q6K_KNOWN_SUM
+
+
+def test_dequant_raw_random_bytes(gpu):
+    """Arbitrary code / scale bytes (finite f16 scales), including subnormal f16 scales."""
+    rng = np.random.default_rng(5)
+    for t, bs, n in ((quant.Q4_K, 144, 256), (quant.Q5_K, 176, 256), (quant.Q6_K, 210, 256), (quant.Q8_0, 34, 32)):
+        raw = rng.integers(0, 256, (64, bs), dtype=np.uint8)
+        sub = np.frombuffer(np.uint16(0x0123).tobytes(), np.uint8)  # an f16 subnormal
+        if t == quant.Q6_K:
+            raw[:, 208:210] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+            raw[::3, 208:210] = sub
+        elif t == quant.Q8_0:
+            raw[:, 0:2] = np.frombuffer(np.float16(0.02).tobytes(), np.uint8)
+            raw[::3, 0:2] = sub
+        else:
+            raw[:, 0:2] = np.frombuffer(np.float16(0.03).tobytes(), np.uint8)
+            raw[:, 2:4] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+            raw[::3, 2:4] = sub
+        flat = raw.reshape(-1)
+        assert np.array_equal(bits(gpu.dequant(t, flat, 64 * n)), bits(oracle.dequant(t, flat, 64 * n))), t
+
+
+@pytest.mark.parametrize("t", FORMATS)
+@pytest.mark.parametrize("K,N", [(768, 2304), (3072, 768)])
+def test_weight_planes_dequant_bitexact(gpu, t, K, N):
+    """The GEMM's decoder on the uploaded planes reproduces DequantWeightMatrix bit for bit."""
+    rng = np.random.default_rng(K + N + t)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    blocks = quant.quantize(t, w, rng)
+    W = gpu.Weight(t, blocks, K, N)
+    got = W.dequant()
+    ref = oracle.dequant(t, blocks.reshape(-1), N * K).reshape(N, K)
+    assert np.array_equal(bits(got), bits(ref))
+
+
+def test_weight_q5k_alias_types(gpu):
+    """DequantWeightMatrix maps ggml types 13, 15 and 16 to Q5_K (gemm.go:241)."""
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((128, 256)) * 0.02).astype(np.float32)
+    blocks = quant.quantize(quant.Q5_K, w)
+    ref = gpu.Weight(quant.Q5_K, blocks, 256, 128).dequant()
+    for alias in (15, 16):
+        assert np.array_equal(bits(gpu.Weight(alias, blocks, 256, 128).dequant()), bits(ref))
+
+
+def _gemm_case(t, K, N, M, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    blocks = quant.quantize(t, w, rng)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    Wd = oracle.dequant(t, blocks.reshape(-1), N * K).reshape(N, K)
+    return blocks, X, Wd
+
+
+SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+
+
+@pytest.mark.parametrize("t", FORMATS)
+@pytest.mark.parametrize("K,N", SHAPES)
+@pytest.mark.parametrize("M", [8, 512])
+def test_gemm_vs_oracle(gpu, t, K, N, M):
+    """Config 2: Y = X W^T against the reference GemmPrePacked32 order on the dequantised W.
+    f16 rounding of X and W gives a relative error ~2e-4 rms per output, so we require
+    rms(Y - Yref) <= 1e-3 * rms(Yref) and max|Y - Yref| <= 1e-2 * max|Yref|."""
+    blocks, X, Wd = _gemm_case(t, K, N, M, 7 * K + N + M + t)
+    W = gpu.Weight(t, blocks, K, N)
+    Y = W.gemm(X)
+    ref = oracle.gemm(X, Wd)
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    err = Y.astype(np.float64) - ref
+    assert float(np.sqrt(np.mean(err ** 2))) <= 1e-3 * rms
+    assert float(np.abs(err).max()) <= 1e-2 * float(np.abs(ref).max())
+
+
+@pytest.mark.parametrize("t", [quant.Q8_0, quant.Q4_K, quant.Q6_K])
+def test_gemm_row_invariance(gpu, t):
+    """A row's output bits do not depend on M or on which kernel (small-M split-K or large-M
+    tiles) computed it: the canonical 256-wide chunk order is shared by both."""
+    K, N = 3072, 768
+    blocks, X, _ = _gemm_case(t, K, N, 300, 99 + t)
+    W = gpu.Weight(t, blocks, K, N)
+    big = W.gemm(X)
+    for rows in ([0], [5, 17, 299], list(range(64)), list(range(40, 120))):
+        part = W.gemm(X[rows])
+        assert np.array_equal(bits(part), bits(big[rows])), rows
+
+
+def test_gemm_large_m_rows_vs_oracle(gpu):
+    """M = 32768 (config 2's largest): sampled rows against the oracle, plus row invariance."""
+    t, K, N, M = quant.Q8_0, 768, 2304, 32768
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    blocks = quant.quantize(t, w, rng)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    W = gpu.Weight(t, blocks, K, N)
+    Y = W.gemm(X)
+    rows = np.sort(rng.choice(M, 48, replace=False))
+    Wd = oracle.dequant(t, blocks.reshape(-1), N * K).reshape(N, K)
+    ref = oracle.gemm(X[rows], Wd)
+    err = Y[rows].astype(np.float64) - ref
+    assert float(np.sqrt(np.mean(err ** 2))) <= 1e-3 * float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    assert np.array_equal(bits(W.gemm(X[rows])), bits(Y[rows]))
+
+
+def test_weight_errors(gpu):
+    with pytest.raises(gpu.LLEError):
+        gpu.Weight(2, np.zeros(1024, np.uint8), 256, 128)  # Q4_0: not on the path
+    with pytest.raises(gpu.LLEError):
+        gpu.Weight(quant.Q8_0, np.zeros(34 * 10, np.uint8), 320, 1)  # N not a multiple of 128
