@@ -1,0 +1,187 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X encoder forward (one JSON line on stdout).
+
+Headline workload (BASELINE.json metric "embeddings/sec at B=256,L=128 Q8_0"): config 4 —
+full 12-layer nomic-bert, random-init N(0, 0.02) Q8_0 GGUF, B=256 sequences of L=128 tokens,
+every position valid. A step = one batched forward (embedding gather ... mean-pool + L2) over
+the batch, with ids/mask already resident in HBM and the embeddings left in HBM.
+
+Also reported: p50/p90 latency of config 1 (B=1, L=8; host-synchronised per call), per-kernel
+HIP-event times, the dominant kernel's roofline fraction (measured live with HIP events on
+the stream the kernels run on) and the CPU oracle's embeddings/s on a bounded sample of the
+same workload, timed on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "llm-embed_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--latency-iters", type=int, default=200)
+    ap.add_argument("--cpu-seqs", type=int, default=16, help="sequences in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--mix", default="Q8_0")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); sequences are "
+              "independent, so N GPUs would each run this same workload on B/N sequences.", file=sys.stderr)
+        sys.exit(2)
+
+    import llmembed
+    from llmembed import _hip, synth
+    from llmembed._lib import check, lib
+
+    llmembed.init(0)
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
+    spec = synth.ModelSpec()
+    path = synth.model_path(spec, args.mix, synth.CONFIG_SEED + 4)
+    log(f"[bench] model {os.path.basename(path)}")
+    emb = llmembed.Embedder.load(path)
+    model = emb.model()
+    L_ = lib()
+
+    # ---------------------------------------------------------------- config 4 throughput
+    ids, mask = synth.config_inputs(4)
+    B, L = ids.shape
+    D = model.hidden_dim
+    d_ids, d_mask = _hip.DeviceBuffer.from_array(ids), _hip.DeviceBuffer.from_array(mask)
+    d_out = _hip.DeviceBuffer(B * D * 4)
+    stream = _hip.Stream()
+
+    def step():
+        check(L_.lle_embed_batch_async(model.h, d_ids.ptr, d_mask.ptr, B, L, D, d_out.ptr, stream.h))
+
+    for _ in range(args.warmup):
+        step()
+    _hip.synchronize()
+    model.set_timing(True)  # HIP events around every launch, on `stream`
+    _hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    _hip.synchronize()
+    t1 = time.perf_counter()
+    kt = model.timing()
+    model.set_timing(False)
+    sec = t1 - t0
+    value = B * args.steps / sec
+    ms_per_step = 1000.0 * sec / args.steps
+    out = d_out.download((B, D), np.float32)
+    norms = np.linalg.norm(out.astype(np.float64), axis=1)
+    assert np.all(np.isfinite(out)) and np.abs(norms - 1).max() < 1e-3, "bench output is not L2-normalised"
+    log(f"[bench] c4: {value:.1f} emb/s, {ms_per_step:.3f} ms/step")
+
+    kernels = {k: dict(avg_ms=v["total_ms"] / max(v["launches"], 1), launches_per_step=v["launches"] / args.steps,
+                       share=v["total_ms"] / max(sum(x["total_ms"] for x in kt.values()), 1e-9))
+               for k, v in kt.items()}
+    for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["share"]):
+        log(f"[bench]   {k:12s} avg {v['avg_ms']:.4f} ms  x{v['launches_per_step']:.0f}/step  {100 * v['share']:.1f}%")
+    # dominant kernel: the one with the largest share of the step
+    dom = max(kt.items(), key=lambda kv: kv[1]["total_ms"])
+    dname, dv = dom
+    avg_s = dv["total_ms"] / dv["launches"] / 1000.0
+    T = B * L
+    if dname.startswith("gemm"):
+        K_, N_ = {"gemm_qkv": (D, 3 * D), "gemm_out": (D, D), "gemm_upgate": (D, 2 * model.ffn_dim),
+                  "gemm_down": (model.ffn_dim, D)}[dname]
+        flops = 2.0 * T * N_ * K_  # every position of config 4 is a valid token
+        roof = dict(kernel=dname, bound="mfma", achieved=flops / avg_s / 1e12, peak=PEAK_F16_TFLOPS, unit="TFLOP/s",
+                    frac=flops / avg_s / 1e12 / PEAK_F16_TFLOPS, traffic=None,
+                    per_launch=f"2*M*N*K = 2*{T}*{N_}*{K_} FLOP", avg_launch_ms=avg_s * 1e3)
+    else:
+        roof = dict(kernel=dname, bound="hbm", achieved=dv["bytes"] / dv["launches"] / avg_s / 1e9, peak=PEAK_HBM_GBS,
+                    unit="GB/s", frac=dv["bytes"] / dv["launches"] / avg_s / 1e9 / PEAK_HBM_GBS, traffic=None,
+                    avg_launch_ms=avg_s * 1e3)
+    total_flops = 226492416.0 * T + 4.0 * D * model.num_layers * B * L * L
+    model_tflops = total_flops / (sec / args.steps) / 1e12
+
+    # ---------------------------------------------------------------- config 1 latency
+    ids1, mask1 = synth.config_inputs(1)
+    d_ids1, d_mask1 = _hip.DeviceBuffer.from_array(ids1), _hip.DeviceBuffer.from_array(mask1)
+    d_out1 = _hip.DeviceBuffer(D * 4)
+    L1 = ids1.shape[1]
+
+    def step1():
+        check(L_.lle_embed_batch_async(model.h, d_ids1.ptr, d_mask1.ptr, 1, L1, D, d_out1.ptr, stream.h))
+        stream.synchronize()
+
+    for _ in range(20):
+        step1()
+    lat = []
+    for _ in range(args.latency_iters):
+        a = time.perf_counter()
+        step1()
+        lat.append(time.perf_counter() - a)
+    lat = np.array(lat) * 1e3
+    p50, p90 = float(np.percentile(lat, 50)), float(np.percentile(lat, 90))
+    log(f"[bench] c1 latency p50 {p50:.3f} ms p90 {p90:.3f} ms")
+
+    # ---------------------------------------------------------------- CPU baseline
+    cpu = None
+    if args.cpu_seqs > 0:
+        import oracle
+
+        om = oracle.OracleModel(path)
+        S = min(args.cpu_seqs, B)
+        om.embed_batch(ids[:1], mask[:1])  # warm-up (page in the dequantised weights)
+        a = time.perf_counter()
+        ref = om.embed_batch(ids[:S], mask[:S])
+        cs = time.perf_counter() - a
+        try:
+            ncores = len(os.sched_getaffinity(0))
+        except AttributeError:  # pragma: no cover
+            ncores = os.cpu_count()
+        workers = min(os.cpu_count() or 1, S, 8)
+        cos = np.sum(ref * out[:S], axis=1) / np.linalg.norm(ref, axis=1) / np.linalg.norm(out[:S], axis=1)
+        cpu = dict(value=S / cs, unit="embeddings/s", cores=min(ncores, workers * min(os.cpu_count() or 1, 8)),
+                   kind="port",
+                   sample=(f"C oracle (restatement of the reference pure-Go AVX-512 GemmPrePacked32 path) on the first "
+                           f"{S} of the {B} config-4 sequences (L={L}), {workers} EmbedBatch workers x "
+                           f"{min(os.cpu_count() or 1, 8)} GEMM threads, {cs:.1f} s wall on {ncores} available cores"),
+                   gpu_vs_cpu_min_cos=float(cos.min()))
+        log(f"[bench] cpu oracle {S / cs:.2f} emb/s ({cs:.1f} s); min cos vs GPU {cos.min():.7f}")
+
+    res = {
+        "metric": "embeddings/sec at B=256,L=128 Q8_0",
+        "value": value,
+        "unit": "embeddings/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"config 4: full 12-layer nomic-bert (d=768, 12 heads, FFN 3072), random-init "
+                               f"N(0,0.02) {args.mix} GGUF, B={B}, L={L}, all positions valid",
+                   "batch": B, "seq_len": L, "quant": args.mix},
+        "model_tflops": model_tflops,
+        "p50_ms_b1_l8": p50,
+        "p90_ms_b1_l8": p90,
+        "kernels": kernels,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "gpu_vs_cpu": (value / cpu["value"]) if cpu else None,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
