@@ -9,9 +9,9 @@
 //   * Canonical reduction order, identical in every kernel variant so that a row's result
 //     never depends on M, the tile it lands in or the batch it belongs to (the reference's
 //     EmbedBatch == Embed contract, internal/embed/embedder_test.go:139-144):
-//       K is cut into 256-wide chunks; inside a chunk one MFMA chain starting from 0 walks
-//       64-wide steps (two 32-wide MFMAs each) in increasing k; the chunk results are added
-//       into a running f32 total that starts at 0, in chunk order.
+//       K is cut into chunks (768 wide when K % 768 == 0, else 256); inside a chunk one MFMA
+//       chain starting from 0 walks 64-wide steps (two 32-wide MFMAs each) in increasing k;
+//       the chunk results are added into a running f32 total that starts at 0, in order.
 //   * MFMA operand roles: A = W rows (features), B = X rows (tokens), so D[feature][token];
 //     lane l holds features 4*(l/16)+r (r = 0..3) of token l%16.
 //   * Epilogues: plain f32 store, residual add, QKV split + RoPE + head-major f16 scatter,
@@ -25,7 +25,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int KSTEP = 64;   // K per LDS stage
-constexpr int KCHUNK = 256; // canonical reduction chunk
 constexpr int LDP = 8;      // LDS row padding (halfs): 144 B rows spread 16 rows over all banks
 
 struct GemmP {
@@ -40,7 +39,7 @@ struct GemmP {
   const float* rope_sin;
   int L, Lp, H, D;
   __half* g;
-  float* part;  // split-K partials [K/KCHUNK][M][N]
+  float* part;  // split-K partials [K/kchunk][M][N]
 };
 
 // GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42).
@@ -113,10 +112,17 @@ __device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const 
 }
 
 // ---------------------------------------------------------------------------------------
+// Canonical chunk of the K reduction: 768 when K is a multiple of 768 (every nomic-bert
+// projection), else 256. Both kernel families derive it from K alone.
+__host__ __device__ constexpr int kchunk_of(int K) { return (K % 768 == 0) ? 768 : 256; }
+
 // Large-M kernel: BM x BN block tile, 4 waves in WM x WN, LDS double buffer over 64-wide K
 // steps, dequantisation at LDS-store time (each weight decoded once per block tile).
-template <int FMT, int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(256) void gemm_big(GemmP p) {
+// MULTI = K spans more than one canonical chunk (then a second accumulator set holds the
+// running total). Two blocks per CU (launch bounds) so one block's loads overlap the other's
+// MFMAs.
+template <int FMT, int BM, int BN, int WM, int WN, int EPI, bool MULTI>
+__global__ __launch_bounds__(256, 2) void gemm_big(GemmP p) {
   constexpr int TM = BM / WM, TN = BN / WN, FB = TN / 16, TB = TM / 16;
   constexpr int LDW = KSTEP + LDP;
   constexpr int XCH = BM * (KSTEP / 8);   // 16-byte chunks of the X tile
@@ -131,15 +137,20 @@ __global__ __launch_bounds__(256) void gemm_big(GemmP p) {
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int M = p.M, K = p.K;
   const int KT = K / KSTEP;
+  const int steps_per_chunk = kchunk_of(K) / KSTEP;
 
-  floatx4 acc[FB][TB], tot[FB][TB];
+  floatx4 acc[FB][TB];
+  floatx4 tot[MULTI ? FB : 1][MULTI ? TB : 1];
 #pragma unroll
   for (int i = 0; i < FB; i++)
 #pragma unroll
-    for (int j = 0; j < TB; j++) {
-      acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-      tot[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < TB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (MULTI) {
+#pragma unroll
+    for (int i = 0; i < FB; i++)
+#pragma unroll
+      for (int j = 0; j < TB; j++) tot[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
 
   uint4 xr[XPT];
   RawSeg wr[WPT];
@@ -197,14 +208,16 @@ __global__ __launch_bounds__(256) void gemm_big(GemmP p) {
 #pragma unroll
         for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
     }
-    if (((kt + 1) * KSTEP) % KCHUNK == 0 || kt + 1 == KT) {
+    if constexpr (MULTI) {
+      if ((kt + 1) % steps_per_chunk == 0) {
 #pragma unroll
-      for (int i = 0; i < FB; i++)
+        for (int i = 0; i < FB; i++)
 #pragma unroll
-        for (int j = 0; j < TB; j++) {
-          tot[i][j] += acc[i][j];
-          acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+          for (int j = 0; j < TB; j++) {
+            tot[i][j] += acc[i][j];
+            acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+          }
+      }
     }
     if (kt + 1 < KT) sstore(st ^ 1, kt + 1);
     __syncthreads();
@@ -215,72 +228,97 @@ __global__ __launch_bounds__(256) void gemm_big(GemmP p) {
     const int m = m0 + wm * TM + j * 16 + lr;
     if (m < M) {
 #pragma unroll
-      for (int i = 0; i < FB; i++) epilogue<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, tot[i][j]);
+      for (int i = 0; i < FB; i++) {
+        floatx4 v;
+        if constexpr (MULTI) {
+          v = tot[i][j];
+        } else {
+          v = floatx4{0.f, 0.f, 0.f, 0.f};
+          v += acc[i][j];  // total = 0 + chunk, as the split-K reduction computes it
+        }
+        epilogue<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, v);
+      }
     }
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// Small-M kernel (M <= 64): one block per (64-row feature tile, 256-wide K chunk); all of
-// the block's weights and activations are requested up front (one memory round trip), the
-// chunk's MFMA chain result goes to part[chunk][m][n]; gemm_reduce adds the chunks in order.
-template <int FMT, int BM>
+// Small-M kernel (M <= 64): one block per (64-row feature tile, canonical K chunk). Every
+// global load of the block is issued before the first MFMA (one memory round trip); the chunk
+// goes through LDS in 256-wide pieces while a single MFMA chain continues across them. The
+// chunk result goes to part[chunk][m][n]; gemm_reduce adds the chunks in order.
+template <int FMT, int BM, int NPIECE>
 __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
-  constexpr int BN = 64, TB = BM / 16;
-  constexpr int LDW = KCHUNK + LDP;
-  constexpr int WU = BN * (KCHUNK / 16);  // 1024 segments
+  constexpr int BN = 64, TB = BM / 16, PK = 256;
+  constexpr int LDW = PK + LDP;
+  constexpr int WU = BN * (PK / 16);  // 1024 segments per piece
   constexpr int WPT = WU / 256;
-  constexpr int XCH = BM * (KCHUNK / 8);
+  constexpr int XCH = BM * (PK / 8);
   constexpr int XPT = (XCH + 255) / 256;
+  constexpr bool AHEAD = FMT != 0;  // f32 weights are too wide to hold every piece in registers
+  constexpr int NP = AHEAD ? NPIECE : 1;
   __shared__ __attribute__((aligned(16))) _Float16 sW[BN][LDW];
   __shared__ __attribute__((aligned(16))) _Float16 sX[BM][LDW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * BN, c = blockIdx.y, kbase = c * KCHUNK;
+  const int n0 = blockIdx.x * BN, c = blockIdx.y, kbase = c * NPIECE * PK;
   const int M = p.M, K = p.K;
 
-  RawSeg wr[WPT];
-  uint4 xr[XPT];
+  RawSeg wr[NP][WPT];
+  uint4 xr[NP][XPT];
+  auto load_piece = [&](int slot, int kb) {
 #pragma unroll
-  for (int i = 0; i < WPT; i++) {
-    const int u = tid + i * 256;
-    wr[i] = load_seg<FMT>(p.w, n0 + (u >> 4), kbase + (u & 15) * 16);
-  }
-#pragma unroll
-  for (int i = 0; i < XPT; i++) {
-    const int cc = tid + i * 256;
-    if (cc < XCH) {
-      const int row = cc >> 5, ch = cc & 31;
-      xr[i] = row < M ? *(const uint4*)(p.x + (size_t)row * K + kbase + ch * 8) : uint4{0, 0, 0, 0};
+    for (int i = 0; i < WPT; i++) {
+      const int u = tid + i * 256;
+      wr[slot][i] = load_seg<FMT>(p.w, n0 + (u >> 4), kb + (u & 15) * 16);
     }
-  }
 #pragma unroll
-  for (int i = 0; i < XPT; i++) {
-    const int cc = tid + i * 256;
-    if (cc < XCH) *(uint4*)&sX[cc >> 5][(cc & 31) * 8] = xr[i];
-  }
+    for (int i = 0; i < XPT; i++) {
+      const int cc = tid + i * 256;
+      if (cc < XCH) {
+        const int row = cc >> 5, ch = cc & 31;
+        xr[slot][i] = row < M ? *(const uint4*)(p.x + (size_t)row * K + kb + ch * 8) : uint4{0, 0, 0, 0};
+      }
+    }
+  };
+  if constexpr (AHEAD) {
 #pragma unroll
-  for (int i = 0; i < WPT; i++) {
-    const int u = tid + i * 256;
-    float v[16];
-    decode_seg<FMT>(wr[i], kbase + (u & 15) * 16, v);
-    uint4* dst = (uint4*)&sW[u >> 4][(u & 15) * 16];
-    dst[0] = pack8(v);
-    dst[1] = pack8(v + 8);
+    for (int pc = 0; pc < NPIECE; pc++) load_piece(pc, kbase + pc * PK);
   }
-  __syncthreads();
 
   const int lr = lane & 15, lk = (lane >> 4) * 8;
   floatx4 acc[TB];
 #pragma unroll
   for (int j = 0; j < TB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < KCHUNK / 32; ks++) {
-    const half8 af = *(const half8*)&sW[wave * 16 + lr][ks * 32 + lk];
+  for (int pc = 0; pc < NPIECE; pc++) {
+    const int slot = AHEAD ? pc : 0;
+    const int kb = kbase + pc * PK;
+    if constexpr (!AHEAD) load_piece(0, kb);
+    if (pc > 0) __syncthreads();
 #pragma unroll
-    for (int j = 0; j < TB; j++) {
-      const half8 bf = *(const half8*)&sX[j * 16 + lr][ks * 32 + lk];
-      acc[j] = mfma16(af, bf, acc[j]);
+    for (int i = 0; i < XPT; i++) {
+      const int cc = tid + i * 256;
+      if (cc < XCH) *(uint4*)&sX[cc >> 5][(cc & 31) * 8] = xr[slot][i];
+    }
+#pragma unroll
+    for (int i = 0; i < WPT; i++) {
+      const int u = tid + i * 256;
+      float v[16];
+      decode_seg<FMT>(wr[slot][i], kb + (u & 15) * 16, v);
+      uint4* dst = (uint4*)&sW[u >> 4][(u & 15) * 16];
+      dst[0] = pack8(v);
+      dst[1] = pack8(v + 8);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < PK / 32; ks++) {
+      const half8 af = *(const half8*)&sW[wave * 16 + lr][ks * 32 + lk];
+#pragma unroll
+      for (int j = 0; j < TB; j++) {
+        const half8 bf = *(const half8*)&sX[j * 16 + lr][ks * 32 + lk];
+        acc[j] = mfma16(af, bf, acc[j]);
+      }
     }
   }
   float* part = p.part + (size_t)c * M * p.N;
@@ -297,31 +335,40 @@ __global__ __launch_bounds__(256) void gemm_reduce(GemmP p) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= p.M * nq) return;
   const int m = idx / nq, f = (idx - m * nq) * 4;
-  const int nch = p.K / KCHUNK;
+  const int nch = p.K / kchunk_of(p.K);
   floatx4 t = floatx4{0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < nch; c++) t += *(const floatx4*)(p.part + ((size_t)c * p.M + m) * p.N + f);
   epilogue<EPI>(p, m, f, t);
 }
 
 // ---------------------------------------------------------------------------------------
+template <int FMT, int BM, int EPI>
+static hipError_t launch_small(const GemmP& p, hipStream_t st) {
+  const int kc = kchunk_of(p.K);
+  dim3 grid(p.N / 64, p.K / kc);
+  if (kc == 768)
+    hipLaunchKernelGGL((gemm_small<FMT, BM, 3>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_small<FMT, BM, 1>), grid, dim3(256), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int n = p.M * (p.N / 4);
+  hipLaunchKernelGGL((gemm_reduce<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
 template <int FMT, int EPI>
 static hipError_t launch_fmt(const GemmP& p, hipStream_t st) {
   if (p.M <= 64) {
-    dim3 grid(p.N / 64, p.K / KCHUNK);
-    if (p.M <= 16)
-      hipLaunchKernelGGL((gemm_small<FMT, 16>), grid, dim3(256), 0, st, p);
-    else if (p.M <= 32)
-      hipLaunchKernelGGL((gemm_small<FMT, 32>), grid, dim3(256), 0, st, p);
-    else
-      hipLaunchKernelGGL((gemm_small<FMT, 64>), grid, dim3(256), 0, st, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int n = p.M * (p.N / 4);
-    hipLaunchKernelGGL((gemm_reduce<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, p);
-    return hipGetLastError();
+    if (p.M <= 16) return launch_small<FMT, 16, EPI>(p, st);
+    if (p.M <= 32) return launch_small<FMT, 32, EPI>(p, st);
+    return launch_small<FMT, 64, EPI>(p, st);
   }
   dim3 grid(p.N / 128, (p.M + 127) / 128);
-  hipLaunchKernelGGL((gemm_big<FMT, 128, 128, 2, 2, EPI>), grid, dim3(256), 0, st, p);
+  if (p.K > kchunk_of(p.K))
+    hipLaunchKernelGGL((gemm_big<FMT, 128, 128, 2, 2, EPI, true>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_big<FMT, 128, 128, 2, 2, EPI, false>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

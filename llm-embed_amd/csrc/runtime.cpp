@@ -129,7 +129,8 @@ static int ensure_ws(lle_model* m, int B, int L) {
   const size_t T = (size_t)B * L;
   const int Lp = (L + 63) / 64 * 64;
   const size_t heads = (size_t)B * m->H * Lp * 64;
-  const size_t kd = (size_t)m->D / 256, kf = (size_t)m->F / 256;
+  auto nch = [](int K) { return (size_t)(K % 768 == 0 ? K / 768 : K / 256); };
+  const size_t kd = nch(m->D), kf = nch(m->F);
   const size_t part = T <= 64 ? (size_t)64 * std::max({kd * 3 * m->D, kd * 2 * m->F, kf * m->D}) : 0;
   if (T <= m->ws_T && heads <= m->ws_heads && part <= m->ws_part && B <= m->ws_B) return LLE_OK;
   const size_t nT = std::max(T, m->ws_T), nH = std::max(heads, m->ws_heads), nP = std::max(part, m->ws_part);
@@ -789,7 +790,7 @@ int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y) {
   hipError_t e = hipMalloc(&dX, M * K * 4);
   if (e == hipSuccess) e = hipMalloc(&dx16, M * K * 2);
   if (e == hipSuccess) e = hipMalloc(&dY, M * N * 4);
-  if (e == hipSuccess && M <= 64) e = hipMalloc(&dP, (K / 256) * (size_t)M * N * 4);
+  if (e == hipSuccess && M <= 64) e = hipMalloc(&dP, (K % 768 == 0 ? K / 768 : K / 256) * (size_t)M * N * 4);
   int rc = LLE_OK;
   if (e != hipSuccess) rc = fail(LLE_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
   if (!rc && hipMemcpy(dX, X, M * K * 4, hipMemcpyHostToDevice) != hipSuccess) rc = fail(LLE_EDEVICE, "copy X");
