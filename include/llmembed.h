@@ -152,6 +152,9 @@ int32_t lle_weight_destroy(lle_weight* w);
 /* Test hook: the uploaded (re-laid-out) weight dequantised by the GEMM's own decoder,
  * as f32 [N][K] (must equal DequantWeightMatrix bit for bit). */
 int32_t lle_weight_dequant(const lle_weight* w, float* out);
+/* Test hook: the same weight as the GEMM's f16 MFMA operand, f16 bits [N][K]; every value is
+ * the f32 dequantisation rounded once to f16 (round-to-nearest-even). */
+int32_t lle_weight_dequant_f16(const lle_weight* w, uint16_t* out);
 /* Host pointers, synchronous. */
 int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y);
 /* Device pointers: X f32 [M][K] is converted to f16 into d_x16 (M*K halfs, caller-owned),

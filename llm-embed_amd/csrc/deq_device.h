@@ -184,4 +184,116 @@ __device__ __forceinline__ void decode_seg(const RawSeg& r, int k0, float* v) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Decode a segment straight to f16 (the GEMM operand). Every value equals the f32 decode
+// above rounded once to f16 (round-to-nearest-even).
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ half2_t bits_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+__device__ __forceinline__ uint32_t pack_rn(float a, float b) {
+  half2_t h;
+  h.x = (_Float16)a;
+  h.y = (_Float16)b;
+  return h2_bits(h);
+}
+
+template <int FMT>
+__device__ __forceinline__ void decode_seg_h(const RawSeg& r, int k0, uint4& lo, uint4& hi) {
+  if constexpr (FMT == 8) {
+    // q (int8) is exact in f16: bytes biased to q+128 are placed in the mantissa of 1024.0
+    // (0x6400), giving 1024 + q + 128; subtracting 1152 leaves q exactly. q * d then rounds the
+    // exact product once in f16, which is the f32 product (exact) rounded to f16.
+    const half2_t d2 = bits_h2((r.x & 0xffffu) * 0x10001u);
+    const half2_t bias = bits_h2(0x64806480u);  // 1152.0 in both halves
+    uint32_t o[8];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const uint32_t u = u4_word(r.q, w) ^ 0x80808080u;
+      const half2_t a = bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x05010400u)) - bias;
+      const half2_t b = bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x05030402u)) - bias;
+      o[2 * w] = h2_bits(a * d2);
+      o[2 * w + 1] = h2_bits(b * d2);
+    }
+    lo = uint4{o[0], o[1], o[2], o[3]};
+    hi = uint4{o[4], o[5], o[6], o[7]};
+  } else {
+    float v[16];
+    decode_seg<FMT>(r, k0, v);
+    lo = uint4{pack_rn(v[0], v[1]), pack_rn(v[2], v[3]), pack_rn(v[4], v[5]), pack_rn(v[6], v[7])};
+    hi = uint4{pack_rn(v[8], v[9]), pack_rn(v[10], v[11]), pack_rn(v[12], v[13]), pack_rn(v[14], v[15])};
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Buffer-resource loads for the large-M GEMM: every per-lane byte offset is loop-invariant and
+// the per-K-step advance is a wave-uniform scalar offset, so a tile load costs no VALU.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+struct WRsrc {
+  __amdgpu_buffer_rsrc_t r0, r1, r2, r3;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return uint4{t.x, t.y, t.z, t.w};
+}
+
+// Lane-invariant offsets of segment s (0..3, elements 16s..16s+15 of a 64-wide K step) of row n.
+struct SegOff {
+  int o0, o1, o2, o3;
+};
+
+template <int FMT>
+__device__ __forceinline__ SegOff seg_off(int N, int K, int n, int s) {
+  SegOff o{0, 0, 0, 0};
+  if constexpr (FMT == 8) {
+    o.o0 = ((s >> 1) * N + n) * 32 + (s & 1) * 16;
+    o.o1 = ((s >> 1) * N + n) * 2;
+  } else if constexpr (FMT == 12 || FMT == 13) {
+    o.o0 = n * 32 + 16 * (s & 1);
+    o.o1 = n * 16;
+    o.o2 = n * 8 + 4 * (s >> 1);
+  } else if constexpr (FMT == 14) {
+    o.o0 = n * 32 + 16 * (s & 1);
+    o.o1 = n * 16 + 4 * s;
+    o.o2 = n * 4 + s;
+    o.o3 = n * 2;
+  } else {
+    o.o0 = (n * K + 16 * s) * 4;
+  }
+  return o;
+}
+
+// Load segment (n, s) of 64-wide K step kt.
+template <int FMT>
+__device__ __forceinline__ RawSeg load_seg_buf(const WRsrc& w, const SegOff& o, int N, int kt) {
+  RawSeg r;
+  if constexpr (FMT == 8) {
+    r.q = buf_load16(w.r0, o.o0, kt * 2 * N * 32);
+    r.x = __builtin_amdgcn_raw_buffer_load_b16(w.r1, o.o1, kt * 2 * N * 2, 0);
+  } else if constexpr (FMT == 12 || FMT == 13) {
+    r.q = buf_load16(w.r0, o.o0, kt * N * 32);
+    r.hdr = buf_load16(w.r1, o.o1, (kt >> 2) * N * 16);
+    if constexpr (FMT == 13) r.x = __builtin_amdgcn_raw_buffer_load_b32(w.r2, o.o2, kt * N * 8, 0);
+  } else if constexpr (FMT == 14) {
+    r.q = buf_load16(w.r0, o.o0, kt * N * 32);
+    r.x = __builtin_amdgcn_raw_buffer_load_b32(w.r1, o.o1, kt * N * 16, 0);
+    const uint32_t sc = __builtin_amdgcn_raw_buffer_load_b8(w.r2, o.o2, kt * N * 4, 0);
+    const uint32_t d = __builtin_amdgcn_raw_buffer_load_b16(w.r3, o.o3, (kt >> 2) * N * 2, 0);
+    r.y = sc | (d << 16);
+  } else {
+    r.q = buf_load16(w.r0, o.o0, kt * 256);
+    r.hdr = buf_load16(w.r0, o.o0 + 16, kt * 256);
+    r.f32b = buf_load16(w.r0, o.o0 + 32, kt * 256);
+    r.f32c = buf_load16(w.r0, o.o0 + 48, kt * 256);
+  }
+  return r;
+}
+
 }  // namespace lle

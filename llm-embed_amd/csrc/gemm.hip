@@ -16,6 +16,8 @@
 //     lane l holds features 4*(l/16)+r (r = 0..3) of token l%16.
 //   * Epilogues: plain f32 store, residual add, QKV split + RoPE + head-major f16 scatter,
 //     and GeLU(gate) * up on the row-interleaved up||gate matrix.
+#include <type_traits>
+
 #include "deq_device.h"
 #include "lle_internal.h"
 
@@ -25,7 +27,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int KSTEP = 64;   // K per LDS stage
-constexpr int LDP = 8;      // LDS row padding (halfs): 144 B rows spread 16 rows over all banks
 
 struct GemmP {
   WPlanes w;
@@ -111,6 +112,11 @@ __device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const 
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// LDS tiles are rows of 16-byte chunks; chunk c of row r is stored at c ^ (r & 7). A wave's
+// ds_read_b128 of 16 rows x one chunk then spreads over all banks (measured on gfx950: 1.8x the
+// read bandwidth of 16-byte-padded rows).
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+
 // ---------------------------------------------------------------------------------------
 // Canonical chunk of the K reduction: 768 when K is a multiple of 768 (every nomic-bert
 // projection), else 256. Both kernel families derive it from K alone.
@@ -121,14 +127,17 @@ __host__ __device__ constexpr int kchunk_of(int K) { return (K % 768 == 0) ? 768
 // MULTI = K spans more than one canonical chunk (then a second accumulator set holds the
 // running total). Two blocks per CU (launch bounds) so one block's loads overlap the other's
 // MFMAs.
-template <int FMT, int BM, int BN, int WM, int WN, int EPI, bool MULTI>
-__global__ __launch_bounds__(256, 2) void gemm_big(GemmP p) {
+// LA = load lookahead in K steps (register sets in flight): 2 for 128-wide feature tiles, 1 for
+// 256-wide ones whose 128 accumulators leave room for a single set.
+template <int FMT, int BM, int BN, int WM, int WN, int EPI, bool MULTI, int LA>
+__global__ __launch_bounds__(WM * WN * 64, 512 / (WM * WN * 64)) void gemm_big(GemmP p) {
+  constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN, FB = TN / 16, TB = TM / 16;
-  constexpr int LDW = KSTEP + LDP;
+  constexpr int LDW = KSTEP;  // 128-byte rows, 16-byte chunks XOR-swizzled by row (swz)
   constexpr int XCH = BM * (KSTEP / 8);   // 16-byte chunks of the X tile
-  constexpr int XPT = (XCH + 255) / 256;
+  constexpr int XPT = XCH / NT;
   constexpr int WU = BN * (KSTEP / 16);   // 16-element W segments
-  constexpr int WPT = (WU + 255) / 256;
+  constexpr int WPT = WU / NT;
   __shared__ __attribute__((aligned(16))) _Float16 sW[2][BN][LDW];
   __shared__ __attribute__((aligned(16))) _Float16 sX[2][BM][LDW];
 
@@ -152,62 +161,118 @@ __global__ __launch_bounds__(256, 2) void gemm_big(GemmP p) {
       for (int j = 0; j < TB; j++) tot[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  uint4 xr[XPT];
-  RawSeg wr[WPT];
+  static_assert(XCH % NT == 0 && WU % NT == 0, "tile loads must cover whole passes of the block");
+  // Two register sets of prefetched data: set s holds K step j with j % 2 == s. Iteration kt
+  // computes step kt from LDS, stores step kt+1 (loaded one iteration earlier) into the other
+  // LDS stage and issues the loads of step kt+2, so each load has two steps of MFMA work to
+  // arrive. Loads are buffer loads with loop-invariant lane offsets; rows past M re-read row
+  // M-1 (those rows only feed output rows that are never stored).
+  uint4 xr[LA][XPT];
+  RawSeg wr[LA][WPT];
+  const int lr = lane & 15, lg = lane >> 4;
 
-  auto gload = [&](int kt) {
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x);
+  const WRsrc rw{make_rsrc(p.w.p0), make_rsrc(p.w.p1), make_rsrc(p.w.p2), make_rsrc(p.w.p3)};
+  int xoff[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int c = tid + i * NT;
+    xoff[i] = (min(m0 + (c >> 3), M - 1) * K + (c & 7) * 8) * 2;
+  }
+  // W segment u: row u % BN, segment u / BN, so a wave's LDS stores hit consecutive rows
+  SegOff woff[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; i++) {
+    const int u = tid + i * NT;
+    woff[i] = seg_off<FMT>(p.N, K, n0 + u % BN, u / BN);
+  }
+
+  auto gload = [&](auto S, int kt) {
+    constexpr int s = decltype(S)::value;
+#pragma unroll
+    for (int i = 0; i < XPT; i++) xr[s][i] = buf_load16(rx, xoff[i], kt * KSTEP * 2);
+#pragma unroll
+    for (int i = 0; i < WPT; i++) wr[s][i] = load_seg_buf<FMT>(rw, woff[i], p.N, kt);
+  };
+  // store register set `set` (holding K step kt) into LDS stage `st`
+  auto sstore = [&](auto SET, auto ST, int kt) {
+    constexpr int set = decltype(SET)::value, st = decltype(ST)::value;
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
-      const int c = tid + i * 256;
-      if (c < XCH) {
-        const int row = c >> 3, ch = c & 7, m = m0 + row;
-        xr[i] = m < M ? *(const uint4*)(p.x + (size_t)m * K + kt * KSTEP + ch * 8) : uint4{0, 0, 0, 0};
-      }
+      const int c = tid + i * NT;
+      *(uint4*)&sX[st][c >> 3][swz(c >> 3, c & 7) * 8] = xr[set][i];
     }
 #pragma unroll
     for (int i = 0; i < WPT; i++) {
-      const int u = tid + i * 256;
-      if (u < WU) wr[i] = load_seg<FMT>(p.w, n0 + (u >> 2), kt * KSTEP + (u & 3) * 16);
+      const int u = tid + i * NT;
+      const int row = u % BN, sg = u / BN;
+      uint4 lo, hi;
+      decode_seg_h<FMT>(wr[set][i], kt * KSTEP + sg * 16, lo, hi);
+      *(uint4*)&sW[st][row][swz(row, 2 * sg) * 8] = lo;
+      *(uint4*)&sW[st][row][swz(row, 2 * sg + 1) * 8] = hi;
     }
   };
-  auto sstore = [&](int st, int kt) {
+  // One K step on LDS stage S: all 16 operand fragments are read first; the decode + LDS store
+  // of the next stage (sstore) is interleaved between the first half's MFMAs so the VALU and
+  // ds_write work overlaps the matrix pipe instead of running while it idles.
+  // One K step on LDS stage S, storing register set SET (K step kt+1) into stage SN on the way.
+  // LA = 2: every fragment is read first and the store is interleaved with the first half's
+  // MFMAs (its loads were issued a step earlier). LA = 1: fragments are read per half and the
+  // store waits until the second half, giving this step's loads half a step more to land.
+  auto step = [&](auto S, auto SN, auto SET, int kt, bool store_next) {
+    constexpr int s = decltype(S)::value;
+    if constexpr (LA == 2) {
+      half8 af[2][FB], bf[2][TB];
 #pragma unroll
-    for (int i = 0; i < XPT; i++) {
-      const int c = tid + i * 256;
-      if (c < XCH) *(uint4*)&sX[st][c >> 3][(c & 7) * 8] = xr[i];
-    }
+      for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
-    for (int i = 0; i < WPT; i++) {
-      const int u = tid + i * 256;
-      if (u < WU) {
-        float v[16];
-        decode_seg<FMT>(wr[i], kt * KSTEP + (u & 3) * 16, v);
-        uint4* dst = (uint4*)&sW[st][u >> 2][(u & 3) * 16];
-        dst[0] = pack8(v);
-        dst[1] = pack8(v + 8);
+        for (int i = 0; i < FB; i++) af[ks][i] = *(const half8*)&sW[s][wn * TN + i * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+#pragma unroll
+        for (int j = 0; j < TB; j++) bf[ks][j] = *(const half8*)&sX[s][wm * TM + j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
       }
-    }
-  };
-
-  gload(0);
-  sstore(0, 0);
-  __syncthreads();
-  const int lr = lane & 15, lk = (lane >> 4) * 8;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      half8 af[FB], bf[TB];
-#pragma unroll
-      for (int i = 0; i < FB; i++) af[i] = *(const half8*)&sW[st][wn * TN + i * 16 + lr][ks * 32 + lk];
-#pragma unroll
-      for (int j = 0; j < TB; j++) bf[j] = *(const half8*)&sX[st][wm * TM + j * 16 + lr][ks * 32 + lk];
 #pragma unroll
       for (int i = 0; i < FB; i++)
 #pragma unroll
-        for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[0][i], bf[0][j], acc[i][j]);
+      if (store_next) sstore(SET, SN, kt + 1);
+      // ds_read all fragments, then per MFMA of the first half: two VALU ops and some ds_writes
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FB + TB), 0);
+#pragma unroll
+      for (int i = 0; i < FB * TB; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < FB; i++)
+#pragma unroll
+        for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[1][i], bf[1][j], acc[i][j]);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        half8 af[FB], bf[TB];
+#pragma unroll
+        for (int i = 0; i < FB; i++) af[i] = *(const half8*)&sW[s][wn * TN + i * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+#pragma unroll
+        for (int j = 0; j < TB; j++) bf[j] = *(const half8*)&sX[s][wm * TM + j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+#pragma unroll
+        for (int i = 0; i < FB; i++)
+#pragma unroll
+          for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+        if (ks == 1 && store_next) {
+          sstore(SET, SN, kt + 1);
+          __builtin_amdgcn_sched_group_barrier(0x100, FB + TB, 0);
+#pragma unroll
+          for (int i = 0; i < FB * TB; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+          }
+        }
+      }
     }
+  };
+  auto chunk_end = [&](int kt) {
     if constexpr (MULTI) {
       if ((kt + 1) % steps_per_chunk == 0) {
 #pragma unroll
@@ -219,8 +284,60 @@ __global__ __launch_bounds__(256, 2) void gemm_big(GemmP p) {
           }
       }
     }
-    if (kt + 1 < KT) sstore(st ^ 1, kt + 1);
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+
+  // KT is a multiple of 4 (K % 256 == 0), so the loop runs in pairs of steps (stage indices
+  // stay compile-time constants). The last pair is peeled: inside the loop every path issues
+  // the same loads, so the compiler's vmcnt waits count only the older set.
+  if constexpr (LA == 2) {
+    gload(S0{}, 0);
+    gload(S1{}, 1);
+    sstore(S0{}, S0{}, 0);
     __syncthreads();
+    int kt = 0;
+    for (; kt < KT - 2; kt += 2) {
+      gload(S0{}, kt + 2);  // set 0 <- step kt+2
+      __builtin_amdgcn_sched_barrier(0);
+      step(S0{}, S1{}, S1{}, kt, true);  // compute stage 0, store set 1 (step kt+1) -> stage 1
+      chunk_end(kt);
+      __syncthreads();
+      gload(S1{}, kt + 3);  // set 1 <- step kt+3
+      __builtin_amdgcn_sched_barrier(0);
+      step(S1{}, S0{}, S0{}, kt + 1, true);  // compute stage 1, store set 0 (step kt+2) -> stage 0
+      chunk_end(kt + 1);
+      __syncthreads();
+    }
+    step(S0{}, S1{}, S1{}, kt, true);
+    chunk_end(kt);
+    __syncthreads();
+    step(S1{}, S0{}, S0{}, kt + 1, false);
+    chunk_end(kt + 1);
+  } else {
+    gload(S0{}, 0);
+    sstore(S0{}, S0{}, 0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt < KT - 2; kt += 2) {
+      gload(S0{}, kt + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      step(S0{}, S1{}, S0{}, kt, true);  // compute stage 0, store step kt+1 -> stage 1
+      chunk_end(kt);
+      __syncthreads();
+      gload(S0{}, kt + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      step(S1{}, S0{}, S0{}, kt + 1, true);  // compute stage 1, store step kt+2 -> stage 0
+      chunk_end(kt + 1);
+      __syncthreads();
+    }
+    gload(S0{}, kt + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    step(S0{}, S1{}, S0{}, kt, true);
+    chunk_end(kt);
+    __syncthreads();
+    step(S1{}, S0{}, S0{}, kt + 1, false);
+    chunk_end(kt + 1);
   }
 
 #pragma unroll
@@ -250,7 +367,7 @@ __global__ __launch_bounds__(256, 2) void gemm_big(GemmP p) {
 template <int FMT, int BM, int NPIECE>
 __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
   constexpr int BN = 64, TB = BM / 16, PK = 256;
-  constexpr int LDW = PK + LDP;
+  constexpr int LDW = PK;  // XOR-swizzled chunks (swz)
   constexpr int WU = BN * (PK / 16);  // 1024 segments per piece
   constexpr int WPT = WU / 256;
   constexpr int XCH = BM * (PK / 8);
@@ -286,7 +403,7 @@ __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
     for (int pc = 0; pc < NPIECE; pc++) load_piece(pc, kbase + pc * PK);
   }
 
-  const int lr = lane & 15, lk = (lane >> 4) * 8;
+  const int lr = lane & 15, lg = lane >> 4;
   floatx4 acc[TB];
 #pragma unroll
   for (int j = 0; j < TB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -299,24 +416,23 @@ __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
       const int cc = tid + i * 256;
-      if (cc < XCH) *(uint4*)&sX[cc >> 5][(cc & 31) * 8] = xr[slot][i];
+      if (cc < XCH) *(uint4*)&sX[cc >> 5][swz(cc >> 5, cc & 31) * 8] = xr[slot][i];
     }
 #pragma unroll
     for (int i = 0; i < WPT; i++) {
-      const int u = tid + i * 256;
-      float v[16];
-      decode_seg<FMT>(wr[slot][i], kb + (u & 15) * 16, v);
-      uint4* dst = (uint4*)&sW[u >> 4][(u & 15) * 16];
-      dst[0] = pack8(v);
-      dst[1] = pack8(v + 8);
+      const int u = tid + i * 256, row = u >> 4, sg = u & 15;
+      uint4 lo, hi;
+      decode_seg_h<FMT>(wr[slot][i], kb + sg * 16, lo, hi);
+      *(uint4*)&sW[row][swz(row, 2 * sg) * 8] = lo;
+      *(uint4*)&sW[row][swz(row, 2 * sg + 1) * 8] = hi;
     }
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < PK / 32; ks++) {
-      const half8 af = *(const half8*)&sW[wave * 16 + lr][ks * 32 + lk];
+      const half8 af = *(const half8*)&sW[wave * 16 + lr][swz(lr, ks * 4 + lg) * 8];
 #pragma unroll
       for (int j = 0; j < TB; j++) {
-        const half8 bf = *(const half8*)&sX[j * 16 + lr][ks * 32 + lk];
+        const half8 bf = *(const half8*)&sX[j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
         acc[j] = mfma16(af, bf, acc[j]);
       }
     }
@@ -364,11 +480,27 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st) {
     if (p.M <= 32) return launch_small<FMT, 32, EPI>(p, st);
     return launch_small<FMT, 64, EPI>(p, st);
   }
+  const bool multi = p.K > kchunk_of(p.K);
+  if (p.M >= 1024) {
+    if (!multi && p.N >= 4096 && p.N % 256 == 0) {
+      // 256 x 256 tiles: each X tile is read by half as many blocks, each decoded weight feeds
+      // 256 tokens, and the 64 x 128 wave tiles need fewer LDS bytes per MAC
+      dim3 grid(p.N / 256, (p.M + 255) / 256);
+      hipLaunchKernelGGL((gemm_big<FMT, 256, 256, 4, 2, EPI, false, 1>), grid, dim3(512), 0, st, p);
+      return hipGetLastError();
+    }
+    dim3 grid(p.N / 128, (p.M + 255) / 256);
+    if (multi)
+      hipLaunchKernelGGL((gemm_big<FMT, 256, 128, 4, 2, EPI, true, 2>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_big<FMT, 256, 128, 4, 2, EPI, false, 2>), grid, dim3(512), 0, st, p);
+    return hipGetLastError();
+  }
   dim3 grid(p.N / 128, (p.M + 127) / 128);
-  if (p.K > kchunk_of(p.K))
-    hipLaunchKernelGGL((gemm_big<FMT, 128, 128, 2, 2, EPI, true>), grid, dim3(256), 0, st, p);
+  if (multi)
+    hipLaunchKernelGGL((gemm_big<FMT, 128, 128, 2, 2, EPI, true, 2>), grid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((gemm_big<FMT, 128, 128, 2, 2, EPI, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_big<FMT, 128, 128, 2, 2, EPI, false, 2>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -426,6 +558,35 @@ __global__ void dequant_weight_kernel(WPlanes w, float* out) {
 #pragma unroll
     for (int i = 0; i < 16; i++) o[i] = v[i];
   }
+}
+
+// The GEMM operand decode (f16) of an uploaded weight: out f16 bits [N][K].
+template <int FMT>
+__global__ void dequant_weight_h_kernel(WPlanes w, uint4* out) {
+  const int64_t nseg = (int64_t)w.N * (w.K / 16);
+  for (int64_t s = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; s < nseg; s += (int64_t)gridDim.x * blockDim.x) {
+    const int n = (int)(s / (w.K / 16)), k0 = (int)(s % (w.K / 16)) * 16;
+    RawSeg r = load_seg<FMT>(w, n, k0);
+    uint4 lo, hi;
+    decode_seg_h<FMT>(r, k0, lo, hi);
+    out[((size_t)n * w.K + k0) / 8] = lo;
+    out[((size_t)n * w.K + k0) / 8 + 1] = hi;
+  }
+}
+
+hipError_t launch_dequant_weight_h(const WeightDev& wd, uint16_t* out, hipStream_t st) {
+  WPlanes w{wd.p0, wd.p1, wd.p2, wd.p3, wd.K, wd.N};
+  dim3 g(1024), b(256);
+  uint4* o = (uint4*)out;
+  switch (wd.type) {
+    case LLE_TYPE_Q8_0: hipLaunchKernelGGL((dequant_weight_h_kernel<8>), g, b, 0, st, w, o); break;
+    case LLE_TYPE_Q4_K: hipLaunchKernelGGL((dequant_weight_h_kernel<12>), g, b, 0, st, w, o); break;
+    case LLE_TYPE_Q5_K: hipLaunchKernelGGL((dequant_weight_h_kernel<13>), g, b, 0, st, w, o); break;
+    case LLE_TYPE_Q6_K: hipLaunchKernelGGL((dequant_weight_h_kernel<14>), g, b, 0, st, w, o); break;
+    case LLE_TYPE_F32: hipLaunchKernelGGL((dequant_weight_h_kernel<0>), g, b, 0, st, w, o); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_dequant_weight(const WeightDev& wd, float* out, hipStream_t st) {

@@ -82,6 +82,7 @@ hipError_t launch_f32_to_f16(const float* x, __half* y, int64_t n, hipStream_t s
 hipError_t launch_f16_to_f32_bits(const uint16_t* h, float* out, int64_t n, hipStream_t st);
 hipError_t launch_dequant_raw(int type, const uint8_t* blocks, int64_t n, float* out, hipStream_t st);
 hipError_t launch_dequant_weight(const WeightDev& w, float* out, hipStream_t st);
+hipError_t launch_dequant_weight_h(const WeightDev& w, uint16_t* out, hipStream_t st);
 
 struct EmbedArgs {
   const int32_t* ids;

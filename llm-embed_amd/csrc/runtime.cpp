@@ -763,6 +763,20 @@ int32_t lle_weight_dequant(const lle_weight* w, float* out) {
   return LLE_OK;
 }
 
+int32_t lle_weight_dequant_f16(const lle_weight* w, uint16_t* out) {
+  if (!w || !out) return fail(LLE_EINVAL, "null argument");
+  LLE_HIP(hipSetDevice(w->device));
+  void* d = nullptr;
+  const size_t n = (size_t)w->w.K * w->w.N;
+  LLE_HIP(hipMalloc(&d, n * 2));
+  hipError_t e = launch_dequant_weight_h(w->w, (uint16_t*)d, w->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+  if (e == hipSuccess) e = hipMemcpy(out, d, n * 2, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(LLE_EDEVICE, std::string("weight dequant f16: ") + hipGetErrorString(e));
+  return LLE_OK;
+}
+
 static int gemm_enqueue(const lle_weight* w, const float* dX, void* dx16, int M, float* dY, float* part, hipStream_t st) {
   LAUNCH(launch_f32_to_f16(dX, (__half*)dx16, (int64_t)M * w->w.K, st));
   GemmArgs g{};

@@ -18,7 +18,7 @@ EXPORTS = [
     "lle_model_create", "lle_model_load_gguf", "lle_model_destroy", "lle_model_dims", "lle_embed",
     "lle_embed_batch", "lle_embed_batch_async", "lle_forward_hidden", "lle_model_status",
     "lle_model_set_timing", "lle_model_get_timing", "lle_weight_create", "lle_weight_destroy",
-    "lle_weight_dequant", "lle_gemm", "lle_gemm_async",
+    "lle_weight_dequant", "lle_weight_dequant_f16", "lle_gemm", "lle_gemm_async",
 ]
 
 ERRORS = {-1: "EINVAL", -2: "EDEVICE", -3: "ENOMEM", -4: "EUNSUPPORTED", -5: "EIO", -6: "ENOTFOUND"}
@@ -82,6 +82,7 @@ def lib(path: str | None = None):
         "lle_weight_create": ([I32, P, I32, I32, C.POINTER(P)], I32),
         "lle_weight_destroy": ([P], I32),
         "lle_weight_dequant": ([P, P], I32),
+        "lle_weight_dequant_f16": ([P, P], I32),
         "lle_gemm": ([P, P, I32, P], I32),
         "lle_gemm_async": ([P, P, P, I32, P, P], I32),
     }
@@ -142,6 +143,12 @@ class Weight:
         out = np.empty((self.N, self.K), np.float32)
         check(lib().lle_weight_dequant(self.h, ptr(out)))
         return out
+
+    def dequant_f16(self) -> np.ndarray:
+        """The GEMM's f16 operand values of this weight, [N][K] float16."""
+        out = np.empty((self.N, self.K), np.uint16)
+        check(lib().lle_weight_dequant_f16(self.h, ptr(out)))
+        return out.view(np.float16)
 
     def gemm(self, X: np.ndarray) -> np.ndarray:
         X = np.ascontiguousarray(X, np.float32)

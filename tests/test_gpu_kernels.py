@@ -79,6 +79,37 @@ def test_weight_planes_dequant_bitexact(gpu, t, K, N):
     assert np.array_equal(bits(got), bits(ref))
 
 
+@pytest.mark.parametrize("t", FORMATS)
+def test_weight_planes_f16_operand_bitexact(gpu, t):
+    """The f16 MFMA operand of every weight equals the reference's f32 dequantisation rounded
+    once to f16 (RNE, numpy's float32 -> float16), including subnormal f16 scales."""
+    K, N = 768, 256
+    rng = np.random.default_rng(40 + t)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w[:8] *= 1e-4  # tiny rows: small and subnormal f16 scales and products
+    blocks = quant.quantize(t, w, rng)
+    got = gpu.Weight(t, blocks, K, N).dequant_f16()
+    ref = oracle.dequant(t, blocks.reshape(-1), N * K).reshape(N, K).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def test_weight_q8_0_f16_operand_all_codes(gpu):
+    """Q8_0's packed-f16 decode over every int8 code and a spread of f16 scales (normal,
+    subnormal, large): q * d rounded once in f16 == RNE(f32 q * d)."""
+    scales = np.array([1.0, 0.5, 3.0517578125e-05, 6.1035156e-05, 5.9604645e-08, 2.0e-06, 0.0123, 100.0, -0.75,
+                       7.0e-3, 1.5e-5, 250.0, -3.3e-6, 0.031, 1.0e-7, 60.0], np.float16)
+    N = 128
+    codes = np.tile(np.arange(-128, 128, dtype=np.int16).astype(np.int8), (N, 1))  # 256 codes = 8 blocks / row
+    blk = np.zeros((N, 8, 34), np.uint8)
+    for r in range(N):
+        for b in range(8):
+            blk[r, b, 0:2] = np.frombuffer(scales[(r + b) % len(scales)].tobytes(), np.uint8)
+            blk[r, b, 2:] = codes[r, 32 * b:32 * b + 32].view(np.uint8)
+    got = gpu.Weight(quant.Q8_0, blk.reshape(-1), 256, N).dequant_f16()
+    ref = oracle.dequant(quant.Q8_0, blk.reshape(-1), N * 256).reshape(N, 256).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
 def test_weight_q5k_alias_types(gpu):
     """DequantWeightMatrix maps ggml types 13, 15 and 16 to Q5_K (gemm.go:241)."""
     rng = np.random.default_rng(1)
@@ -121,12 +152,12 @@ def test_gemm_vs_oracle(gpu, t, K, N, M):
 @pytest.mark.parametrize("t", [quant.Q8_0, quant.Q4_K, quant.Q6_K])
 def test_gemm_row_invariance(gpu, t):
     """A row's output bits do not depend on M or on which kernel (small-M split-K or large-M
-    tiles) computed it: the canonical 256-wide chunk order is shared by both."""
+    or 128/256-token tiles) computed it: the canonical chunk order is shared by all of them."""
     K, N = 3072, 768
-    blocks, X, _ = _gemm_case(t, K, N, 300, 99 + t)
+    blocks, X, _ = _gemm_case(t, K, N, 1500, 99 + t)
     W = gpu.Weight(t, blocks, K, N)
-    big = W.gemm(X)
-    for rows in ([0], [5, 17, 299], list(range(64)), list(range(40, 120))):
+    big = W.gemm(X)  # M >= 1024: 256-token tiles
+    for rows in ([0], [5, 17, 299], list(range(64)), list(range(40, 120)), list(range(300, 1400))):
         part = W.gemm(X[rows])
         assert np.array_equal(bits(part), bits(big[rows])), rows
 
