@@ -36,41 +36,47 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* s, float& sc,
 
 // ---------------------------------------------------------------------------------------
 // Raw GGUF layout: element j of a row starting at `row` (row bytes per ByteSize).
+template <int TY>
+__device__ __forceinline__ float deq_raw_t(const uint8_t* row, int j) {
+  if constexpr (TY == 0) {
+    return __uint_as_float(*(const uint32_t*)(row + 4 * j));
+  } else if constexpr (TY == 8) {
+    const uint8_t* b = row + (j >> 5) * 34;
+    const float d = f16_bits_to_f32(b[0] | (b[1] << 8));
+    return (float)(int8_t)b[2 + (j & 31)] * d;
+  } else if constexpr (TY == 12 || TY == 13) {
+    constexpr bool q5 = TY == 13;
+    const uint8_t* b = row + (j >> 8) * (q5 ? 176 : 144);
+    const int e = j & 255, g = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    const float d = f16_bits_to_f32(b[0] | (b[1] << 8));
+    const float dmin = f16_bits_to_f32(b[2] | (b[3] << 8));
+    float sc, m;
+    scale_min_k4(2 * g + hi, b + 4, sc, m);
+    const uint8_t byte = b[(q5 ? 48 : 16) + 32 * g + l];
+    int q = hi ? (byte >> 4) : (byte & 0xF);
+    if (q5) q |= ((b[16 + l] >> (2 * g + hi)) & 1) << 4;
+    return fmaf(d * sc, (float)q, -(dmin * m));
+  } else {
+    static_assert(TY == 14, "raw type");
+    const uint8_t* b = row + (j >> 8) * 210;
+    const int e = j & 255, c = e >> 7, el = e & 127, qq = el >> 5, l = el & 31;
+    const uint8_t qlb = b[64 * c + 32 * (qq & 1) + l];
+    const int lo = (qq >> 1) ? (qlb >> 4) : (qlb & 0xF);
+    const int hi = (b[128 + 32 * c + l] >> (2 * qq)) & 3;
+    const int q = (lo | (hi << 4)) - 32;
+    const float d = f16_bits_to_f32(b[208] | (b[209] << 8));
+    return (d * (float)(int8_t)b[192 + (e >> 4)]) * (float)q;
+  }
+}
+
 __device__ __forceinline__ float deq_raw_elem(int type, const uint8_t* row, int j) {
   switch (type) {
-    case 0:
-      return __uint_as_float(*(const uint32_t*)(row + 4 * j));
-    case 8: {
-      const uint8_t* b = row + (j >> 5) * 34;
-      const float d = f16_bits_to_f32(b[0] | (b[1] << 8));
-      return (float)(int8_t)b[2 + (j & 31)] * d;
-    }
-    case 12:
-    case 13: {
-      const bool q5 = type == 13;
-      const uint8_t* b = row + (j >> 8) * (q5 ? 176 : 144);
-      const int e = j & 255, g = e >> 6, hi = (e >> 5) & 1, l = e & 31;
-      const float d = f16_bits_to_f32(b[0] | (b[1] << 8));
-      const float dmin = f16_bits_to_f32(b[2] | (b[3] << 8));
-      float sc, m;
-      scale_min_k4(2 * g + hi, b + 4, sc, m);
-      const uint8_t byte = b[(q5 ? 48 : 16) + 32 * g + l];
-      int q = hi ? (byte >> 4) : (byte & 0xF);
-      if (q5) q |= ((b[16 + l] >> (2 * g + hi)) & 1) << 4;
-      return fmaf(d * sc, (float)q, -(dmin * m));
-    }
-    case 14: {
-      const uint8_t* b = row + (j >> 8) * 210;
-      const int e = j & 255, c = e >> 7, el = e & 127, qq = el >> 5, l = el & 31;
-      const uint8_t qlb = b[64 * c + 32 * (qq & 1) + l];
-      const int lo = (qq >> 1) ? (qlb >> 4) : (qlb & 0xF);
-      const int hi = (b[128 + 32 * c + l] >> (2 * qq)) & 3;
-      const int q = (lo | (hi << 4)) - 32;
-      const float d = f16_bits_to_f32(b[208] | (b[209] << 8));
-      return (d * (float)(int8_t)b[192 + (e >> 4)]) * (float)q;
-    }
-    default:
-      return __uint_as_float(0x7fc00000u);
+    case 0: return deq_raw_t<0>(row, j);
+    case 8: return deq_raw_t<8>(row, j);
+    case 12: return deq_raw_t<12>(row, j);
+    case 13: return deq_raw_t<13>(row, j);
+    case 14: return deq_raw_t<14>(row, j);
+    default: return __uint_as_float(0x7fc00000u);
   }
 }
 

@@ -364,7 +364,7 @@ __global__ __launch_bounds__(WM * WN * 64, 512 / (WM * WN * 64)) void gemm_big(G
 // global load of the block is issued before the first MFMA (one memory round trip); the chunk
 // goes through LDS in 256-wide pieces while a single MFMA chain continues across them. The
 // chunk result goes to part[chunk][m][n]; gemm_reduce adds the chunks in order.
-template <int FMT, int BM, int NPIECE>
+template <int FMT, int BM, int NPIECE, int EPI, bool DIRECT>
 __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
   constexpr int BN = 64, TB = BM / 16, PK = 256;
   constexpr int LDW = PK;  // XOR-swizzled chunks (swz)
@@ -437,11 +437,24 @@ __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
       }
     }
   }
-  float* part = p.part + (size_t)c * M * p.N;
+  if constexpr (DIRECT) {
+    // single-chunk K: the total is 0 + this chunk, finished here with the epilogue
 #pragma unroll
-  for (int j = 0; j < TB; j++) {
-    const int m = j * 16 + lr;
-    if (m < M) *(floatx4*)(part + (size_t)m * p.N + n0 + wave * 16 + (lane >> 4) * 4) = acc[j];
+    for (int j = 0; j < TB; j++) {
+      const int m = j * 16 + lr;
+      if (m < M) {
+        floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+        v += acc[j];
+        epilogue<EPI>(p, m, n0 + wave * 16 + (lane >> 4) * 4, v);
+      }
+    }
+  } else {
+    float* part = p.part + (size_t)c * M * p.N;
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      const int m = j * 16 + lr;
+      if (m < M) *(floatx4*)(part + (size_t)m * p.N + n0 + wave * 16 + (lane >> 4) * 4) = acc[j];
+    }
   }
 }
 
@@ -458,27 +471,38 @@ __global__ __launch_bounds__(256) void gemm_reduce(GemmP p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// M <= 64. K spanning one canonical chunk: one kernel, epilogue applied in place. Several
+// chunks: per-chunk partials, then gemm_reduce (or, when `reduce` is false, the caller's own
+// ordered reduction, e.g. the fused residual + LayerNorm row kernel).
 template <int FMT, int BM, int EPI>
-static hipError_t launch_small(const GemmP& p, hipStream_t st) {
+static hipError_t launch_small(const GemmP& p, hipStream_t st, bool reduce) {
   const int kc = kchunk_of(p.K);
-  dim3 grid(p.N / 64, p.K / kc);
+  const int nch = p.K / kc;
+  dim3 grid(p.N / 64, nch);
+  if (nch == 1) {
+    if (kc == 768)
+      hipLaunchKernelGGL((gemm_small<FMT, BM, 3, EPI, true>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_small<FMT, BM, 1, EPI, true>), grid, dim3(256), 0, st, p);
+    return hipGetLastError();
+  }
   if (kc == 768)
-    hipLaunchKernelGGL((gemm_small<FMT, BM, 3>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_small<FMT, BM, 3, EPI, false>), grid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((gemm_small<FMT, BM, 1>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_small<FMT, BM, 1, EPI, false>), grid, dim3(256), 0, st, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !reduce) return e;
   const int n = p.M * (p.N / 4);
   hipLaunchKernelGGL((gemm_reduce<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
 template <int FMT, int EPI>
-static hipError_t launch_fmt(const GemmP& p, hipStream_t st) {
+static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
   if (p.M <= 64) {
-    if (p.M <= 16) return launch_small<FMT, 16, EPI>(p, st);
-    if (p.M <= 32) return launch_small<FMT, 32, EPI>(p, st);
-    return launch_small<FMT, 64, EPI>(p, st);
+    if (p.M <= 16) return launch_small<FMT, 16, EPI>(p, st, reduce);
+    if (p.M <= 32) return launch_small<FMT, 32, EPI>(p, st, reduce);
+    return launch_small<FMT, 64, EPI>(p, st, reduce);
   }
   const bool multi = p.K > kchunk_of(p.K);
   if (p.M >= 1024) {
@@ -505,18 +529,18 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st) {
 }
 
 template <int EPI>
-static hipError_t launch_epi(int type, const GemmP& p, hipStream_t st) {
+static hipError_t launch_epi(int type, const GemmP& p, hipStream_t st, bool reduce = true) {
   switch (type) {
-    case LLE_TYPE_Q8_0: return launch_fmt<8, EPI>(p, st);
-    case LLE_TYPE_Q4_K: return launch_fmt<12, EPI>(p, st);
-    case LLE_TYPE_Q5_K: return launch_fmt<13, EPI>(p, st);
-    case LLE_TYPE_Q6_K: return launch_fmt<14, EPI>(p, st);
-    case LLE_TYPE_F32: return launch_fmt<0, EPI>(p, st);
+    case LLE_TYPE_Q8_0: return launch_fmt<8, EPI>(p, st, reduce);
+    case LLE_TYPE_Q4_K: return launch_fmt<12, EPI>(p, st, reduce);
+    case LLE_TYPE_Q5_K: return launch_fmt<13, EPI>(p, st, reduce);
+    case LLE_TYPE_Q6_K: return launch_fmt<14, EPI>(p, st, reduce);
+    case LLE_TYPE_F32: return launch_fmt<0, EPI>(p, st, reduce);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st) {
+static GemmP make_params(const GemmArgs& a) {
   GemmP p;
   p.w = WPlanes{a.w->p0, a.w->p1, a.w->p2, a.w->p3, a.w->K, a.w->N};
   p.x = a.x;
@@ -535,6 +559,11 @@ hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st) {
   p.D = a.d_model;
   p.g = a.g;
   p.part = a.part;
+  return p;
+}
+
+hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st) {
+  const GemmP p = make_params(a);
   switch (epi) {
     case EPI_F32: return launch_epi<EPI_F32>(a.w->type, p, st);
     case EPI_RESID: return launch_epi<EPI_RESID>(a.w->type, p, st);
@@ -542,6 +571,24 @@ hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st) {
     case EPI_GEGLU: return launch_epi<EPI_GEGLU>(a.w->type, p, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+// h += X . W^T, then LayerNorm of h (rows of N = d_model) into h and h16. At M <= 64 with several
+// K chunks the chunk reduction, residual add and LayerNorm run as one row kernel; otherwise the
+// GEMM's residual epilogue is followed by the LayerNorm kernel. Both orders of operations are
+// identical (same reduction order, same add, same LayerNorm), so results do not depend on M.
+hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
+                                hipStream_t st) {
+  const GemmP p = make_params(a);
+  const int nch = p.K / kchunk_of(p.K);
+  if (p.M <= 64 && (nch == 2 || nch == 3 || nch == 4 || nch == 8 || nch == 12)) {
+    hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, false);
+    if (e != hipSuccess) return e;
+    return launch_reduce_resid_ln(p.part, nch, p.M, p.N, p.y, h16, w, b, eps, st);
+  }
+  hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, true);
+  if (e != hipSuccess) return e;
+  return launch_ln(p.y, h16, w, b, eps, p.M, p.N, st);
 }
 
 // ---------------------------------------------------------------------------------------

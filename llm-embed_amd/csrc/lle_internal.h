@@ -77,6 +77,11 @@ struct GemmArgs {
 };
 
 hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st);
+// a.y (= h) += X . W^T, then LayerNorm(h; w, b, eps) into h and h16
+hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
+                                hipStream_t st);
+hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, float* h, __half* h16, const float* w,
+                                  const float* b, float eps, hipStream_t st);
 
 hipError_t launch_f32_to_f16(const float* x, __half* y, int64_t n, hipStream_t st);
 hipError_t launch_f16_to_f32_bits(const uint16_t* h, float* out, int64_t n, hipStream_t st);

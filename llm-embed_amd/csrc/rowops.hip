@@ -18,6 +18,13 @@ __device__ __forceinline__ float wave_sum(float v) {
 // y = (x - mean) * invStd * w + b. One wave per row; element j = lane + 64 i.
 __device__ __forceinline__ void ln_row(float* x, int ne, int D, const float* w, const float* b, float eps,
                                        int lane, float* hrow, __half* h16row) {
+  float wv[MAXE], bv[MAXE];  // issued before the reductions so their latency overlaps them
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) {
+      wv[i] = w[lane + 64 * i];
+      bv[i] = b[lane + 64 * i];
+    }
   float s = 0.f, ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXE; i++)
@@ -35,7 +42,7 @@ __device__ __forceinline__ void ln_row(float* x, int ne, int D, const float* w, 
   for (int i = 0; i < MAXE; i++)
     if (i < ne) {
       const int j = lane + 64 * i;
-      const float y = (x[i] - mean) * inv * w[j] + b[j];
+      const float y = (x[i] - mean) * inv * wv[i] + bv[i];
       hrow[j] = y;
       h16row[j] = __float2half_rn(y);
     }
@@ -43,6 +50,7 @@ __device__ __forceinline__ void ln_row(float* x, int ne, int D, const float* w, 
 
 // Embedding stage (internal/embed/bert.go:220-249, getEmbedding :290-316):
 // h = deq(token_embd[id]) + deq(token_types[0]), then LayerNorm(token_embd_norm).
+template <int TY>
 __global__ __launch_bounds__(256) void embed_ln_kernel(EmbedArgs a) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -59,13 +67,21 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(EmbedArgs a) {
   for (int i = 0; i < MAXE; i++)
     if (i < ne) {
       const int j = lane + 64 * i;
-      x[i] = deq_raw_elem(a.tok_type, row, j) + a.type0[j];
+      x[i] = deq_raw_t<TY>(row, j) + a.type0[j];
     }
   ln_row(x, ne, a.D, a.w, a.b, a.eps, lane, a.h + (size_t)t * a.D, a.h16 + (size_t)t * a.D);
 }
 
 hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(embed_ln_kernel, dim3((a.T + 3) / 4), dim3(256), 0, st, a);
+  const dim3 g((a.T + 3) / 4), blk(256);
+  switch (a.tok_type) {  // one instantiation per format keeps every row load in one basic block
+    case 0: hipLaunchKernelGGL(embed_ln_kernel<0>, g, blk, 0, st, a); break;
+    case 8: hipLaunchKernelGGL(embed_ln_kernel<8>, g, blk, 0, st, a); break;
+    case 12: hipLaunchKernelGGL(embed_ln_kernel<12>, g, blk, 0, st, a); break;
+    case 13: hipLaunchKernelGGL(embed_ln_kernel<13>, g, blk, 0, st, a); break;
+    case 14: hipLaunchKernelGGL(embed_ln_kernel<14>, g, blk, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -90,27 +106,115 @@ hipError_t launch_ln(float* h, __half* h16, const float* w, const float* b, floa
   return hipGetLastError();
 }
 
+// Ordered split-K reduction + residual add + LayerNorm for one row per wave (M <= 64 path);
+// chunk counts: 768-wide chunks of K = 3072 (4) and the other d_ff / d_model ratios listed below.
+// t = 0 + part[0] + part[1] + ... (gemm_reduce's order), h = h + t (the residual epilogue's add),
+// then the LayerNorm of ln_kernel with the same element-to-lane mapping and reduction tree.
+template <int NCH>
+__global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __restrict__ part, int M, int N, float* h,
+                                                              __half* h16, const float* w, const float* b,
+                                                              float eps) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= M) return;
+  const int ne = N / 64;
+  float* row = h + (size_t)t * N;
+  // every load is issued before the first add (one memory round trip); adds in chunk order
+  float pv[MAXE][NCH], x[MAXE];
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) {
+      const int j = lane + 64 * i;
+      x[i] = row[j];
+#pragma unroll
+      for (int c = 0; c < NCH; c++) pv[i][c] = part[((size_t)c * M + t) * N + j];
+    }
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) {
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < NCH; c++) acc += pv[i][c];
+      x[i] = x[i] + acc;
+    }
+  ln_row(x, ne, N, w, b, eps, lane, row, h16 + (size_t)t * N);
+}
+
+hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, float* h, __half* h16, const float* w,
+                                  const float* b, float eps, hipStream_t st) {
+  const dim3 g((M + 3) / 4), blk(256);
+  switch (nch) {
+    case 2: hipLaunchKernelGGL(reduce_resid_ln_kernel<2>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
+    case 3: hipLaunchKernelGGL(reduce_resid_ln_kernel<3>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
+    case 4: hipLaunchKernelGGL(reduce_resid_ln_kernel<4>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
+    case 8: hipLaunchKernelGGL(reduce_resid_ln_kernel<8>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
+    case 12: hipLaunchKernelGGL(reduce_resid_ln_kernel<12>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // MeanPool + L2Normalize (+ Matryoshka truncation and renormalisation):
 // internal/embed/pool.go:8-54, internal/embed/embedder.go:50-68. Rows with mask == 1 are
 // summed in row order in f32 (the reference's order), scaled by float32(1/count); the norm
-// is accumulated in f64. One block per sequence.
+// is accumulated in f64. One block per sequence: the kept rows are first compacted (in order)
+// into an LDS list, then each thread sums 4 adjacent columns with 16 row loads in flight.
+constexpr int POOL_MAXL = 8192;
 __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ mask,
                                                    int L, int D, int out_dim, float* __restrict__ out) {
   const int b = blockIdx.x, tid = threadIdx.x;
   __shared__ double red[256];
-  __shared__ float vals[1024];
-  float cnt = 0.f;
-  for (int j = tid; j < D; j += 256) {
-    float s = 0.f;
-    cnt = 0.f;
-    for (int i = 0; i < L; i++) {
-      if (mask[(size_t)b * L + i] == 1) {
-        s += h[((size_t)b * L + i) * D + j];
-        cnt += 1.f;
+  __shared__ __align__(16) float vals[1024];
+  __shared__ int rows[POOL_MAXL];
+  __shared__ int wcount[5];
+  // ordered compaction of kept rows: per-wave ballot + prefix over the 4 waves
+  int base = 0;
+  for (int i0 = 0; i0 < L; i0 += 256) {
+    const int i = i0 + tid;
+    const bool keep = i < L && mask[(size_t)b * L + i] == 1;
+    const unsigned long long bal = __ballot(keep);
+    const int lane = tid & 63, wv = tid >> 6;
+    if (lane == 0) wcount[wv] = __popcll(bal);
+    __syncthreads();
+    int off = base;
+    for (int w2 = 0; w2 < wv; w2++) off += wcount[w2];
+    if (keep) rows[off + __popcll(bal & ((1ull << lane) - 1ull))] = i;
+    base += wcount[0] + wcount[1] + wcount[2] + wcount[3];
+    __syncthreads();
+  }
+  const int count = base;
+  const float* hb = h + (size_t)b * L * D;
+  const int c0 = 4 * tid;
+  if (c0 < D) {
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    int i = 0;
+    for (; i + 16 <= count; i += 16) {
+      float4 v[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) v[u] = *(const float4*)(hb + (size_t)rows[i + u] * D + c0);
+#pragma unroll
+      for (int u = 0; u < 16; u++) {
+        s.x += v[u].x;
+        s.y += v[u].y;
+        s.z += v[u].z;
+        s.w += v[u].w;
       }
     }
-    if (cnt != 0.f) s *= 1.0f / cnt;
-    vals[j] = s;
+    for (; i < count; i++) {
+      const float4 v = *(const float4*)(hb + (size_t)rows[i] * D + c0);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+    if (count != 0) {
+      const float inv = 1.0f / (float)count;
+      s.x *= inv;
+      s.y *= inv;
+      s.z *= inv;
+      s.w *= inv;
+    }
+    *(float4*)(vals + c0) = s;
   }
   __syncthreads();
   // L2Normalize over the first n values, twice when truncating (embedder.go:65-68)
@@ -140,6 +244,7 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
 
 hipError_t launch_pool(const float* h, const int32_t* mask, int B, int L, int D, int out_dim, float* out,
                        hipStream_t st) {
+  if (L > POOL_MAXL || D > 1024 || D % 4) return hipErrorInvalidValue;
   hipLaunchKernelGGL(pool_kernel, dim3(B), dim3(256), 0, st, h, mask, L, D, out_dim, out);
   return hipGetLastError();
 }

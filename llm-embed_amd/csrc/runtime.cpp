@@ -86,6 +86,16 @@ struct lle_model {
   float* part = nullptr;
   int32_t *ids = nullptr, *mask = nullptr, *kv_range = nullptr, *status = nullptr;
   float* out = nullptr;
+  // HIP graphs of small forwards, keyed by shape, pointers and stream
+  struct GraphEntry {
+    int B, L, out_dim;
+    const void *ids, *mask;
+    void* out;
+    hipStream_t st;
+    hipGraphExec_t exec;
+  };
+  std::vector<GraphEntry> graphs;
+  bool use_graphs = true;
   // timing
   bool timing = false;
   std::vector<lle::Timer> pending;
@@ -103,7 +113,13 @@ static int dev_alloc(lle_model* m, void** p, size_t bytes) {
   return LLE_OK;
 }
 
+static void clear_graphs(lle_model* m) {
+  for (auto& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
+  m->graphs.clear();
+}
+
 static void ws_free(lle_model* m) {
+  clear_graphs(m);
   void* bufs[] = {m->h, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->kv_range, m->out};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
@@ -285,12 +301,8 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
       g.w = &ly.down;
       g.x = m->ff;
       g.y = m->h;
-      Scope s(m, st, "gemm_down", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 8));
-      LAUNCH(launch_gemm(g, EPI_RESID, st));
-    }
-    {
-      Scope s(m, st, "ln", 0, (double)T * D * 10);
-      LAUNCH(launch_ln(m->h, m->h16, ly.onw, ly.onb, m->eps, T, D, st));
+      Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 18));
+      LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, m->h16, st));
     }
   }
   if (d_out) {
@@ -300,12 +312,51 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
   return LLE_OK;
 }
 
+// Forwards of up to this many tokens are captured once into a HIP graph and replayed: they are
+// launch-bound (~90 kernels), and a replay removes the per-kernel host launch cost.
+constexpr int64_t GRAPH_MAX_TOKENS = 4096;
+constexpr size_t GRAPH_CACHE = 32;
+
+static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim,
+                       float* d_out, hipStream_t st) {
+  if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS)
+    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st);
+  for (auto& g : m->graphs)
+    if (g.B == B && g.L == L && g.out_dim == out_dim && g.ids == d_ids && g.mask == d_mask && g.out == d_out &&
+        g.st == st) {
+      LLE_HIP(hipGraphLaunch(g.exec, st));
+      return LLE_OK;
+    }
+  hipGraph_t graph = nullptr;
+  LLE_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  const int rc = forward(m, d_ids, d_mask, B, L, out_dim, d_out, st);
+  const hipError_t e = hipStreamEndCapture(st, &graph);
+  hipGraphExec_t exec = nullptr;
+  if (rc == LLE_OK && e == hipSuccess && graph &&
+      hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    if (m->graphs.size() >= GRAPH_CACHE) {
+      (void)hipGraphExecDestroy(m->graphs.front().exec);
+      m->graphs.erase(m->graphs.begin());
+    }
+    m->graphs.push_back({B, L, out_dim, d_ids, d_mask, d_out, st, exec});
+    LLE_HIP(hipGraphLaunch(exec, st));
+    return LLE_OK;
+  }
+  // capture unavailable: run eagerly from now on
+  if (graph) (void)hipGraphDestroy(graph);
+  (void)hipGetLastError();
+  m->use_graphs = false;
+  return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st);
+}
+
 static int check_batch(lle_model* m, int B, int L) {
   if (!m) return fail(LLE_EINVAL, "null model");
   if (B <= 0 || L <= 0) return fail(LLE_EINVAL, "B and L must be positive");
   if (L > m->max_seq)
     return fail(LLE_EINVAL, "sequence length " + std::to_string(L) + " exceeds context_length " + std::to_string(m->max_seq));
   if ((int64_t)B * L > (int64_t)1 << 26) return fail(LLE_EINVAL, "batch too large");
+  if (L > 8192) return fail(LLE_EUNSUPPORTED, "sequence length above 8192 (the pooling kernel's row list)");
   return LLE_OK;
 }
 
@@ -337,7 +388,7 @@ static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B
     LLE_HIP(hipStreamSynchronize(st));
   }
   LLE_HIP(hipMemsetAsync(m->status, 0, 4, st));
-  if ((rc = forward(m, m->ids, m->mask, B, L, out_dim, out ? m->out : nullptr, st))) return rc;
+  if ((rc = run_forward(m, m->ids, m->mask, B, L, out_dim, out ? m->out : nullptr, st))) return rc;
   const int od = std::min(out_dim, m->D);
   if (out) LLE_HIP(hipMemcpyAsync(out, m->out, (size_t)B * od * 4, hipMemcpyDeviceToHost, st));
   if (hidden) LLE_HIP(hipMemcpyAsync(hidden, m->h, T * m->D * 4, hipMemcpyDeviceToHost, st));
@@ -410,7 +461,7 @@ static void destroy_model(lle_model* m) {
   if (!m) return;
   (void)hipSetDevice(m->device);
   if (m->stream) (void)hipStreamSynchronize(m->stream);
-  ws_free(m);
+  ws_free(m);  // also destroys cached graphs
   for (void* p : m->allocs) (void)hipFree(p);
   for (auto& t : m->pending) {
     (void)hipEventDestroy(t.a);
@@ -483,6 +534,10 @@ static int create_model(const lle_model_desc* d, lle_model** out) {
 
   // token_embd stays in its GGUF layout: rows are gathered, not streamed.
   m->tok_type = d->token_embd.type;
+  // getEmbedding (internal/embed/bert.go:290-316) gathers F32, Q8_0, Q4_K, Q5_K and Q6_K rows
+  // only; the reference fails each Embed on another type, this library fails the load.
+  if (m->tok_type != 0 && m->tok_type != 8 && (m->tok_type < 12 || m->tok_type > 14))
+    return bail(fail(LLE_EUNSUPPORTED, "unsupported embedding type: " + std::to_string(m->tok_type)));
   m->tok_row_bytes = row_bytes(m->tok_type, D);
   const size_t tok_bytes = (size_t)m->tok_row_bytes * m->vocab;
   void* p = nullptr;
@@ -685,7 +740,7 @@ int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t*
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L))) return rc;
   hipStream_t st = stream ? (hipStream_t)stream : m->stream;
-  if ((rc = forward(m, d_ids, d_mask, B, L, out_dim, d_out, st))) return rc;
+  if ((rc = run_forward(m, d_ids, d_mask, B, L, out_dim, d_out, st))) return rc;
   if (m->timing) {
     LLE_HIP(hipStreamSynchronize(st));
     collect_timing(m);
@@ -705,7 +760,7 @@ int32_t lle_model_status(lle_model* m, int32_t* status) {
 int32_t lle_model_set_timing(lle_model* m, int32_t enable) {
   if (!m) return fail(LLE_EINVAL, "null model");
   std::lock_guard<std::mutex> lk(m->mu);
-  m->timing = enable != 0;
+  m->timing = enable != 0;  // timed forwards run eagerly (events around every launch)
   m->totals.clear();
   return LLE_OK;
 }

@@ -142,3 +142,23 @@ def test_errors(gpu, small_spec):
         e.embed(np.zeros(small_spec.ctx + 1, np.int32))
     with pytest.raises(LLEError):
         Embedder.load("/nonexistent/model.gguf")
+
+
+def test_graph_replay_matches_eager(gpu, small_spec):
+    """Small forwards replay a captured HIP graph. Every replay, interleaved with other shapes
+    and with eager (large, and timing-mode) forwards, must equal the eager result bit for bit."""
+    e, o = models(small_spec, "Q8_0")
+    rng = np.random.default_rng(31)
+    a = rng.integers(0, small_spec.vocab, 8).astype(np.int32)
+    b = rng.integers(0, small_spec.vocab, 21).astype(np.int32)
+    big_ids = rng.integers(0, small_spec.vocab, (40, 128)).astype(np.int32)
+    m = e.model()
+    m.set_timing(True)  # timed forwards run eagerly
+    ea, eb = e.embed(a), e.embed(b)
+    m.set_timing(False)
+    big = e.embed_padded(big_ids, np.ones_like(big_ids))  # 5120 tokens: eager
+    for _ in range(5):
+        assert np.array_equal(bits(e.embed(a)), bits(ea))
+        assert np.array_equal(bits(e.embed(b)), bits(eb))
+        assert np.array_equal(bits(e.embed_padded(big_ids, np.ones_like(big_ids))), bits(big))
+    compare(e.embed(a), o.embed(a), "graph replay")
