@@ -53,17 +53,38 @@ __device__ __forceinline__ float gelu_r(float v) {
   return 0.5f * v * (1.0f + th);
 }
 
-// Epilogue for 4 consecutive output features f..f+3 (f % 4 == 0) of token m.
+// Operands an epilogue reads from memory for features f..f+3 of token m: the residual
+// (EPI_RESID) or the RoPE cos/sin pairs (EPI_QKV, Q and K sections). The small-M kernel issues
+// these loads before its main loop so that they do not add a round trip at the end.
 template <int EPI>
-__device__ __forceinline__ void epilogue(const GemmP& p, int m, int f, floatx4 v) {
+__device__ __forceinline__ floatx4 epi_operands(const GemmP& p, int m, int f) {
+  if constexpr (EPI == EPI_RESID) {
+    return *(const floatx4*)(p.y + (size_t)m * p.N + f);
+  } else if constexpr (EPI == EPI_QKV) {
+    const int sec = f / p.D, e = (f - sec * p.D) & 63;
+    const int pos = m - (m / p.L) * p.L;
+    if (sec < 2) {
+      const float* cr = p.rope_cos + (size_t)pos * 32 + (e >> 1);
+      const float* sr = p.rope_sin + (size_t)pos * 32 + (e >> 1);
+      return floatx4{cr[0], sr[0], cr[1], sr[1]};
+    }
+    return floatx4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    return floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// Epilogue for 4 consecutive output features f..f+3 (f % 4 == 0) of token m; `o` holds what
+// epi_operands returned for the same (m, f).
+template <int EPI>
+__device__ __forceinline__ void epilogue_with(const GemmP& p, int m, int f, floatx4 v, floatx4 o) {
   if constexpr (EPI == EPI_F32) {
     *(floatx4*)(p.y + (size_t)m * p.N + f) = v;
   } else if constexpr (EPI == EPI_RESID) {
-    floatx4* dst = (floatx4*)(p.y + (size_t)m * p.N + f);
-    floatx4 h = *dst;
     // hiddens[i][j] += out[i][j]  (internal/embed/bert.go:262-264, 276-278)
+    floatx4 h = o;
     h.x = h.x + v.x; h.y = h.y + v.y; h.z = h.z + v.z; h.w = h.w + v.w;
-    *dst = h;
+    *(floatx4*)(p.y + (size_t)m * p.N + f) = h;
   } else if constexpr (EPI == EPI_QKV) {
     // QKV row = [Q | K | V], heads 64-contiguous (bert.go:332-347); RoPE on Q and K with
     // the position = token index (bert.go:349-353, ops_simd.go:127-137).
@@ -71,9 +92,7 @@ __device__ __forceinline__ void epilogue(const GemmP& p, int m, int f, floatx4 v
     const int sec = f / D, fi = f - sec * D, h = fi >> 6, e = fi & 63;
     const int b = m / p.L, pos = m - b * p.L;
     if (sec < 2) {
-      const float* cr = p.rope_cos + (size_t)pos * 32 + (e >> 1);
-      const float* sr = p.rope_sin + (size_t)pos * 32 + (e >> 1);
-      const float c0 = cr[0], s0 = sr[0], c1 = cr[1], s1 = sr[1];
+      const float c0 = o.x, s0 = o.y, c1 = o.z, s1 = o.w;
       const float a0 = v.x * c0 - v.y * s0, a1 = v.x * s0 + v.y * c0;
       const float a2 = v.z * c1 - v.w * s1, a3 = v.z * s1 + v.w * c1;
       __half* dst = (sec == 0 ? p.q : p.k) + (((size_t)b * p.H + h) * p.Lp + pos) * 64 + e;
@@ -95,6 +114,11 @@ __device__ __forceinline__ void epilogue(const GemmP& p, int m, int f, floatx4 v
     const float o0 = gelu_r(v.y) * v.x, o1 = gelu_r(v.w) * v.z;
     *(__half2*)(p.g + (size_t)m * F + qo) = __floats2half2_rn(o0, o1);
   }
+}
+
+template <int EPI>
+__device__ __forceinline__ void epilogue(const GemmP& p, int m, int f, floatx4 v) {
+  epilogue_with<EPI>(p, m, f, v, epi_operands<EPI>(p, m, f));
 }
 
 __device__ __forceinline__ uint4 pack8(const float* v) {
@@ -360,18 +384,18 @@ __global__ __launch_bounds__(WM * WN * 64, 512 / (WM * WN * 64)) void gemm_big(G
 }
 
 // ---------------------------------------------------------------------------------------
-// Small-M kernel (M <= 64): one block per (64-row feature tile, canonical K chunk). Every
+// Small-M kernel (M <= 64): one block per (BN-row feature tile, canonical K chunk). Every
 // global load of the block is issued before the first MFMA (one memory round trip); the chunk
 // goes through LDS in 256-wide pieces while a single MFMA chain continues across them. The
 // chunk result goes to part[chunk][m][n]; gemm_reduce adds the chunks in order.
-template <int FMT, int BM, int NPIECE, int EPI, bool DIRECT>
-__global__ __launch_bounds__(256) void gemm_small(GemmP p) {
-  constexpr int BN = 64, TB = BM / 16, PK = 256;
+template <int FMT, int BM, int BN, int NPIECE, int EPI, bool DIRECT>
+__global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
+  constexpr int NT = BN * 4, TB = BM / 16, PK = 256;  // one wave per 16 features
   constexpr int LDW = PK;  // XOR-swizzled chunks (swz)
-  constexpr int WU = BN * (PK / 16);  // 1024 segments per piece
-  constexpr int WPT = WU / 256;
+  constexpr int WU = BN * (PK / 16);  // segments per piece
+  constexpr int WPT = WU / NT;
   constexpr int XCH = BM * (PK / 8);
-  constexpr int XPT = (XCH + 255) / 256;
+  constexpr int XPT = (XCH + NT - 1) / NT;
   constexpr bool AHEAD = FMT != 0;  // f32 weights are too wide to hold every piece in registers
   constexpr int NP = AHEAD ? NPIECE : 1;
   __shared__ __attribute__((aligned(16))) _Float16 sW[BN][LDW];
@@ -386,12 +410,12 @@ __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
   auto load_piece = [&](int slot, int kb) {
 #pragma unroll
     for (int i = 0; i < WPT; i++) {
-      const int u = tid + i * 256;
+      const int u = tid + i * NT;
       wr[slot][i] = load_seg<FMT>(p.w, n0 + (u >> 4), kb + (u & 15) * 16);
     }
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
-      const int cc = tid + i * 256;
+      const int cc = tid + i * NT;
       if (cc < XCH) {
         const int row = cc >> 5, ch = cc & 31;
         xr[slot][i] = row < M ? *(const uint4*)(p.x + (size_t)row * K + kb + ch * 8) : uint4{0, 0, 0, 0};
@@ -404,6 +428,12 @@ __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
   }
 
   const int lr = lane & 15, lg = lane >> 4;
+  floatx4 eop[DIRECT ? TB : 1];
+  if constexpr (DIRECT) {
+#pragma unroll
+    for (int j = 0; j < TB; j++)
+      if (j * 16 + lr < M) eop[j] = epi_operands<EPI>(p, j * 16 + lr, n0 + wave * 16 + lg * 4);
+  }
   floatx4 acc[TB];
 #pragma unroll
   for (int j = 0; j < TB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -415,12 +445,12 @@ __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
     if (pc > 0) __syncthreads();
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
-      const int cc = tid + i * 256;
+      const int cc = tid + i * NT;
       if (cc < XCH) *(uint4*)&sX[cc >> 5][swz(cc >> 5, cc & 31) * 8] = xr[slot][i];
     }
 #pragma unroll
     for (int i = 0; i < WPT; i++) {
-      const int u = tid + i * 256, row = u >> 4, sg = u & 15;
+      const int u = tid + i * NT, row = u >> 4, sg = u & 15;
       uint4 lo, hi;
       decode_seg_h<FMT>(wr[slot][i], kb + sg * 16, lo, hi);
       *(uint4*)&sW[row][swz(row, 2 * sg) * 8] = lo;
@@ -445,7 +475,7 @@ __global__ __launch_bounds__(256) void gemm_small(GemmP p) {
       if (m < M) {
         floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
         v += acc[j];
-        epilogue<EPI>(p, m, n0 + wave * 16 + (lane >> 4) * 4, v);
+        epilogue_with<EPI>(p, m, n0 + wave * 16 + lg * 4, v, eop[j]);
       }
     }
   } else {
@@ -476,20 +506,21 @@ __global__ __launch_bounds__(256) void gemm_reduce(GemmP p) {
 // ordered reduction, e.g. the fused residual + LayerNorm row kernel).
 template <int FMT, int BM, int EPI>
 static hipError_t launch_small(const GemmP& p, hipStream_t st, bool reduce) {
+  constexpr int BN = 64;  // 16-feature one-wave blocks measured no faster at M = 8
   const int kc = kchunk_of(p.K);
   const int nch = p.K / kc;
-  dim3 grid(p.N / 64, nch);
+  const dim3 grid(p.N / BN, nch), blk(BN * 4);
   if (nch == 1) {
     if (kc == 768)
-      hipLaunchKernelGGL((gemm_small<FMT, BM, 3, EPI, true>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm_small<FMT, BM, BN, 3, EPI, true>), grid, blk, 0, st, p);
     else
-      hipLaunchKernelGGL((gemm_small<FMT, BM, 1, EPI, true>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((gemm_small<FMT, BM, BN, 1, EPI, true>), grid, blk, 0, st, p);
     return hipGetLastError();
   }
   if (kc == 768)
-    hipLaunchKernelGGL((gemm_small<FMT, BM, 3, EPI, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_small<FMT, BM, BN, 3, EPI, false>), grid, blk, 0, st, p);
   else
-    hipLaunchKernelGGL((gemm_small<FMT, BM, 1, EPI, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_small<FMT, BM, BN, 1, EPI, false>), grid, blk, 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !reduce) return e;
   const int n = p.M * (p.N / 4);
@@ -541,7 +572,7 @@ static hipError_t launch_epi(int type, const GemmP& p, hipStream_t st, bool redu
 }
 
 static GemmP make_params(const GemmArgs& a) {
-  GemmP p;
+  GemmP p{};
   p.w = WPlanes{a.w->p0, a.w->p1, a.w->p2, a.w->p3, a.w->K, a.w->N};
   p.x = a.x;
   p.M = a.M;

@@ -2,51 +2,9 @@
 // f32 <-> f16 helpers and the raw-GGUF dequantisation test kernel.
 #include "deq_device.h"
 #include "lle_internal.h"
+#include "row_device.h"
 
 namespace lle {
-
-constexpr int MAXE = 16;  // elements per lane: d_model <= 1024
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-// LayerNormInPlace (internal/ggml/ops_simd.go:7-24): one-pass sum / sum of squares in f32,
-// var = sumSq/n - mean^2, invStd = float32(1/sqrt(float64(var + eps))),
-// y = (x - mean) * invStd * w + b. One wave per row; element j = lane + 64 i.
-__device__ __forceinline__ void ln_row(float* x, int ne, int D, const float* w, const float* b, float eps,
-                                       int lane, float* hrow, __half* h16row) {
-  float wv[MAXE], bv[MAXE];  // issued before the reductions so their latency overlaps them
-#pragma unroll
-  for (int i = 0; i < MAXE; i++)
-    if (i < ne) {
-      wv[i] = w[lane + 64 * i];
-      bv[i] = b[lane + 64 * i];
-    }
-  float s = 0.f, ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < MAXE; i++)
-    if (i < ne) {
-      s += x[i];
-      ss += x[i] * x[i];
-    }
-  s = wave_sum(s);
-  ss = wave_sum(ss);
-  const float nf = (float)D;
-  const float mean = s / nf;
-  const float var = ss / nf - mean * mean;
-  const float inv = (float)(1.0 / sqrt((double)(var + eps)));
-#pragma unroll
-  for (int i = 0; i < MAXE; i++)
-    if (i < ne) {
-      const int j = lane + 64 * i;
-      const float y = (x[i] - mean) * inv * wv[i] + bv[i];
-      hrow[j] = y;
-      h16row[j] = __float2half_rn(y);
-    }
-}
 
 // Embedding stage (internal/embed/bert.go:220-249, getEmbedding :290-316):
 // h = deq(token_embd[id]) + deq(token_types[0]), then LayerNorm(token_embd_norm).

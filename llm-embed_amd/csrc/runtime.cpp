@@ -283,12 +283,8 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
       g.w = &ly.out;
       g.x = m->attn;
       g.y = m->h;
-      Scope s(m, st, "gemm_out", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 8));
-      LAUNCH(launch_gemm(g, EPI_RESID, st));
-    }
-    {
-      Scope s(m, st, "ln", 0, (double)T * D * 10);
-      LAUNCH(launch_ln(m->h, m->h16, ly.anw, ly.anb, m->eps, T, D, st));
+      Scope s(m, st, "gemm_out_ln", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 18));
+      LAUNCH(launch_gemm_resid_ln(g, ly.anw, ly.anb, m->eps, m->h16, st));
     }
     {
       g.w = &ly.upgate;
