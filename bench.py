@@ -37,6 +37,9 @@ def main():
     ap.add_argument("--latency-iters", type=int, default=200)
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--mix", default="Q8_0")
+    ap.add_argument("--probe-traffic", action="store_true",
+                    help="for rocprofv3 --pmc runs: two config-4 forwards, then one 256 MiB device-to-device copy "
+                         "(the calibration of FETCH_SIZE / WRITE_SIZE); prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); sequences are "
@@ -66,6 +69,17 @@ def main():
 
     def step():
         check(L_.lle_embed_batch_async(model.h, d_ids.ptr, d_mask.ptr, B, L, D, d_out.ptr, stream.h))
+
+    if args.probe_traffic:
+        step()
+        step()
+        n = 256 << 20
+        src, dst = _hip.DeviceBuffer(n), _hip.DeviceBuffer(n)
+        _hip._ok(_hip.rt().hipMemset(src.ptr, 1, n), "hipMemset")
+        _hip._ok(_hip.rt().hipMemcpy(dst.ptr, src.ptr, n, _hip.D2D), "hipMemcpy")
+        _hip.synchronize()
+        log("[bench] traffic probe done: 2 config-4 forwards, 1 copy of 268435456 B")
+        return
 
     for _ in range(args.warmup):
         step()

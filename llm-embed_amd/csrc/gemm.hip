@@ -16,10 +16,12 @@
 //     lane l holds features 4*(l/16)+r (r = 0..3) of token l%16.
 //   * Epilogues: plain f32 store, residual add, QKV split + RoPE + head-major f16 scatter,
 //     and GeLU(gate) * up on the row-interleaved up||gate matrix.
+#include <climits>
 #include <type_traits>
 
 #include "deq_device.h"
 #include "lle_internal.h"
+#include "row_device.h"
 
 namespace lle {
 
@@ -167,7 +169,21 @@ __global__ __launch_bounds__(WM * WN * 64, 512 / (WM * WN * 64)) void gemm_big(G
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  if constexpr (BN < 256) {
+    // XCD-aware tile order: the dispatcher deals workgroups to the 8 XCDs round-robin
+    // (workgroup b runs on XCD b % 8), so give each XCD a contiguous run of tiles, N-fastest:
+    // the feature tiles that share one token tile's X then hit the same XCD's L2 (measured:
+    // 3.5x less L2-miss traffic at N = 2304). Not for the 256-wide tiles of N = 6144: there the
+    // weights of all feature tiles overflow an XCD's L2, while the plain round-robin deal keeps
+    // each XCD on the same three feature tiles. Any bijection is correct; this is only locality.
+    const int nt = gridDim.x, G = gridDim.x * gridDim.y;
+    const int b = blockIdx.x + blockIdx.y * nt, xcd = b & 7, slot = b >> 3;
+    const int q = G >> 3, r = G & 7;
+    const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+    n0 = (t % nt) * BN;
+    m0 = (t / nt) * BM;
+  }
   const int M = p.M, K = p.K;
   const int KT = K / KSTEP;
   const int steps_per_chunk = kchunk_of(K) / KSTEP;
@@ -384,6 +400,174 @@ __global__ __launch_bounds__(WM * WN * 64, 512 / (WM * WN * 64)) void gemm_big(G
 }
 
 // ---------------------------------------------------------------------------------------
+// Full-row GEMM + residual + LayerNorm (h = LN(h + X W^T)) for N = 768: one block owns BM
+// complete rows, so the LayerNorm runs in the epilogue instead of a second pass over h.
+// 8 waves, each 96 features x BM tokens (6 x BM/16 MFMA tiles). K steps of 32 (one MFMA deep):
+// the whole 768-row weight step is 48 KB of LDS, double-buffered. The per-accumulator MFMA
+// sequence, the chunk totals, the residual add and ln_row are those of gemm_big + ln_kernel,
+// so every output bit equals that path's (and the small-M path's).
+// LDS rows are 64 bytes (4 chunks of 16 B); chunk c of row r sits at c ^ swr(r), which spreads
+// a 16-row fragment read over all banks.
+__device__ __forceinline__ int swr(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+constexpr int LN_N = 768, LN_KS = 32, LN_RS = LN_N + 4;  // LN staging row stride (floats)
+
+template <int FMT, int BM>
+__global__ __launch_bounds__(512, 1) void gemm_rowln(GemmP p, const float* __restrict__ lnw,
+                                                     const float* __restrict__ lnb, float eps, __half* h16) {
+  constexpr int NT = 512, WN = 8, TN = LN_N / WN, FB = TN / 16, TB = BM / 16;
+  constexpr int WU = LN_N * (LN_KS / 16);  // 1536 weight segments per step
+  constexpr int WPT = WU / NT;             // 3
+  constexpr int XCH = BM * (LN_KS / 8);    // 16-byte X chunks per step
+  constexpr int W_BYTES = 2 * LN_N * LN_KS * 2, X_BYTES = 2 * BM * LN_KS * 2;
+  constexpr int R_BYTES = 32 * LN_RS * 4;
+  constexpr int SMEM = (W_BYTES + X_BYTES) > R_BYTES ? (W_BYTES + X_BYTES) : R_BYTES;
+  static_assert(WU % NT == 0 && XCH <= NT, "tile loads");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+  typedef _Float16 WStage[LN_N][LN_KS];
+  typedef _Float16 XStage[BM][LN_KS];
+  WStage* sW = (WStage*)smem;
+  XStage* sX = (XStage*)(smem + W_BYTES);
+
+  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = blockIdx.x * BM;
+  const int M = p.M, K = p.K;
+  const int KT = K / LN_KS;
+
+  floatx4 acc[FB][TB];
+#pragma unroll
+  for (int i = 0; i < FB; i++)
+#pragma unroll
+    for (int j = 0; j < TB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x);
+  const WRsrc rw{make_rsrc(p.w.p0), make_rsrc(p.w.p1), make_rsrc(p.w.p2), make_rsrc(p.w.p3)};
+  // X chunk c (threads c < XCH): row c / 4, 8 halves at k = (c % 4) * 8; rows past M re-read M-1
+  const bool xload = tid < XCH;
+  const int xrow = tid >> 2, xch = tid & 3;
+  const int xoff = (min(m0 + xrow, M - 1) * K + xch * 8) * 2;
+  // W segment u = tid + i * NT: row u % 768, segment u / 768 of the 32-wide step; within the
+  // 64-wide plane step that is segment 2 * (step & 1) + u / 768
+  SegOff woff[2][WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; i++) {
+    const int u = tid + i * NT;
+    woff[0][i] = seg_off<FMT>(LN_N, K, u % LN_N, u / LN_N);
+    woff[1][i] = seg_off<FMT>(LN_N, K, u % LN_N, 2 + u / LN_N);
+  }
+
+  uint4 xr[2];
+  RawSeg wr[2][WPT];
+  // set s holds 32-wide step kt, kt % 2 == s
+  auto gload = [&](auto S, int kt) {
+    constexpr int s = decltype(S)::value;
+    if (xload) xr[s] = buf_load16(rx, xoff, kt * LN_KS * 2);
+#pragma unroll
+    for (int i = 0; i < WPT; i++) wr[s][i] = load_seg_buf<FMT>(rw, woff[s][i], LN_N, kt >> 1);
+  };
+  auto sstore = [&](auto S, int kt) {  // register set S (= step kt) -> LDS stage S
+    constexpr int s = decltype(S)::value;
+    if (xload) *(uint4*)&sX[s][xrow][(xch ^ swr(xrow)) * 8] = xr[s];
+#pragma unroll
+    for (int i = 0; i < WPT; i++) {
+      const int u = tid + i * NT, row = u % LN_N, sg = u / LN_N;
+      uint4 lo, hi;
+      decode_seg_h<FMT>(wr[s][i], kt * LN_KS + sg * 16, lo, hi);
+      *(uint4*)&sW[s][row][((2 * sg) ^ swr(row)) * 8] = lo;
+      *(uint4*)&sW[s][row][((2 * sg + 1) ^ swr(row)) * 8] = hi;
+    }
+  };
+  // compute stage S (step kt); store register set SN (step kt + 1) into stage SN on the way
+  auto step = [&](auto S, auto SN, int kt, bool store_next) {
+    constexpr int s = decltype(S)::value;
+    half8 af[FB], bf[TB];
+#pragma unroll
+    for (int i = 0; i < FB; i++) {
+      const int f = wn * TN + i * 16 + lr;
+      af[i] = *(const half8*)&sW[s][f][(lg ^ swr(f)) * 8];
+    }
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      const int t = j * 16 + lr;
+      bf[j] = *(const half8*)&sX[s][t][(lg ^ swr(t)) * 8];
+    }
+#pragma unroll
+    for (int i = 0; i < FB; i++)
+#pragma unroll
+      for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+    if (store_next) sstore(SN, kt + 1);
+    __builtin_amdgcn_sched_group_barrier(0x100, FB + TB, 0);
+#pragma unroll
+    for (int i = 0; i < FB * TB; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+
+  // KT is even (K % 64 == 0); pairs of steps keep stage indices compile-time constants, and the
+  // last pair is peeled so that every in-loop path issues the same loads.
+  gload(S0{}, 0);
+  gload(S1{}, 1);
+  sstore(S0{}, 0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt < KT - 2; kt += 2) {
+    gload(S0{}, kt + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    step(S0{}, S1{}, kt, true);
+    __syncthreads();
+    gload(S1{}, kt + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    step(S1{}, S0{}, kt + 1, true);
+    __syncthreads();
+  }
+  step(S0{}, S1{}, kt, true);
+  __syncthreads();
+  step(S1{}, S0{}, kt + 1, false);
+  __syncthreads();  // every stage read: LDS is free for the row staging
+
+  // Epilogue: x = h + total (the residual epilogue's add) staged per 32 tokens in LDS, then
+  // LayerNorm by ln_row with ln_kernel's element-to-lane mapping (wave w: 4 rows per half).
+  float* sR = (float*)smem;
+#pragma unroll
+  for (int half = 0; half < BM / 32; half++) {
+#pragma unroll
+    for (int j = 2 * half; j < 2 * half + 2; j++) {
+      const int tl = (j - 2 * half) * 16 + lr, m = m0 + j * 16 + lr;
+#pragma unroll
+      for (int i = 0; i < FB; i++) {
+        const int f = wn * TN + i * 16 + lg * 4;
+        floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+        v += acc[i][j];  // total = 0 + chunk
+        floatx4 x = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (m < M) {
+          const floatx4 h = *(const floatx4*)(p.y + (size_t)m * LN_N + f);
+          x.x = h.x + v.x; x.y = h.y + v.y; x.z = h.z + v.z; x.w = h.w + v.w;
+        }
+        *(floatx4*)&sR[tl * LN_RS + f] = x;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int tl = wn * 4 + r, m = m0 + half * 32 + tl;
+      if (m < M) {
+        float x[MAXE];
+#pragma unroll
+        for (int i = 0; i < MAXE; i++)
+          if (i < LN_N / 64) x[i] = sR[tl * LN_RS + lane + 64 * i];
+        ln_row(x, LN_N / 64, LN_N, lnw, lnb, eps, lane, p.y + (size_t)m * LN_N, h16 + (size_t)m * LN_N);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Small-M kernel (M <= 64): one block per (BN-row feature tile, canonical K chunk). Every
 // global load of the block is issued before the first MFMA (one memory round trip); the chunk
 // goes through LDS in 256-wide pieces while a single MFMA chain continues across them. The
@@ -530,6 +714,7 @@ static hipError_t launch_small(const GemmP& p, hipStream_t st, bool reduce) {
 
 template <int FMT, int EPI>
 static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
+  if ((int64_t)p.M * p.K * 2 > INT32_MAX) return hipErrorInvalidValue;  // 32-bit buffer offsets
   if (p.M <= 64) {
     if (p.M <= 16) return launch_small<FMT, 16, EPI>(p, st, reduce);
     if (p.M <= 32) return launch_small<FMT, 32, EPI>(p, st, reduce);
@@ -612,6 +797,19 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
                                 hipStream_t st) {
   const GemmP p = make_params(a);
   const int nch = p.K / kchunk_of(p.K);
+  if ((int64_t)p.M * p.K * 2 > INT32_MAX) return hipErrorInvalidValue;  // 32-bit buffer offsets
+  if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) {
+    const dim3 grid((p.M + 63) / 64), blk(512);
+    switch (a.w->type) {
+      case LLE_TYPE_Q8_0: hipLaunchKernelGGL((gemm_rowln<8, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
+      case LLE_TYPE_Q4_K: hipLaunchKernelGGL((gemm_rowln<12, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
+      case LLE_TYPE_Q5_K: hipLaunchKernelGGL((gemm_rowln<13, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
+      case LLE_TYPE_Q6_K: hipLaunchKernelGGL((gemm_rowln<14, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
+      case LLE_TYPE_F32: hipLaunchKernelGGL((gemm_rowln<0, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   if (p.M <= 64 && (nch == 2 || nch == 3 || nch == 4 || nch == 8 || nch == 12)) {
     hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, false);
     if (e != hipSuccess) return e;

@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <climits>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -351,7 +352,9 @@ static int check_batch(lle_model* m, int B, int L) {
   if (B <= 0 || L <= 0) return fail(LLE_EINVAL, "B and L must be positive");
   if (L > m->max_seq)
     return fail(LLE_EINVAL, "sequence length " + std::to_string(L) + " exceeds context_length " + std::to_string(m->max_seq));
-  if ((int64_t)B * L > (int64_t)1 << 26) return fail(LLE_EINVAL, "batch too large");
+  // the GEMMs address X ([B*L][d_ff] f16 at most) with 32-bit buffer offsets
+  if ((int64_t)B * L * std::max(m->F, m->D) * 2 > INT32_MAX)
+    return fail(LLE_EINVAL, "batch too large: B*L*d_ff*2 bytes must stay below 2^31");
   if (L > 8192) return fail(LLE_EUNSUPPORTED, "sequence length above 8192 (the pooling kernel's row list)");
   return LLE_OK;
 }

@@ -46,7 +46,7 @@ def _ok(rc, what):
         raise RuntimeError(f"{what} failed with hipError {rc}")
 
 
-H2D, D2H = 1, 2
+H2D, D2H, D2D = 1, 2, 3
 
 
 class DeviceBuffer:

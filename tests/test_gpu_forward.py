@@ -84,6 +84,20 @@ def test_batch_invariance(gpu, small_spec):
         assert np.array_equal(bits(big[i]), bits(batch[i]))
 
 
+@pytest.mark.parametrize("mix", ["Q8_0", "Q5_K", "Q6_K", "F32", "Q4_K_M"])
+def test_full_row_layernorm_path_bitexact(gpu, small_spec, mix):
+    """Batches of >= 1024 tokens run the attention output projection as a full-row GEMM with
+    the residual + LayerNorm in its epilogue; each row must equal the same sequence embedded
+    alone (128-token tiles + separate LayerNorm kernel), bit for bit, and match the oracle."""
+    e, o = models(small_spec, mix)
+    rng = np.random.default_rng(44)
+    seqs = [rng.integers(0, small_spec.vocab, n).astype(np.int32) for n in (128, 97, 128, 64, 128, 128, 5, 128, 128)]
+    batch = e.embed_batch(seqs)  # 9 x 128 = 1152 padded tokens
+    for s, b in zip(seqs, batch):
+        assert np.array_equal(bits(e.embed(s)), bits(b)), len(s)
+    compare(batch[1], o.embed(seqs[1]), f"{mix} full-row LN")
+
+
 def test_padded_batch_vs_oracle(gpu, small_spec):
     """Config-3 style: right-padded batch with per-row lengths, Q4_K_M."""
     e, o = models(small_spec, "Q4_K_M")
