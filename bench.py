@@ -29,6 +29,23 @@ PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "encoder_c4_q8_0_hbm_traffic.md")
+
+
+def committed_traffic(scope):
+    """HBM bytes per launch of a kernel scope, from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE passes, each scaled by its calibration copy). None if absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 6 and cells[0] == scope:
+                    return int(cells[4].replace(",", "")), os.path.relpath(TRAFFIC_PROFILE, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,8 +132,9 @@ def main():
         K_, N_ = {"gemm_qkv": (D, 3 * D), "gemm_out_ln": (D, D), "gemm_upgate": (D, 2 * model.ffn_dim),
                   "gemm_down_ln": (model.ffn_dim, D)}[dname]
         flops = 2.0 * T * N_ * K_  # every position of config 4 is a valid token
+        traffic, tsrc = committed_traffic(dname)
         roof = dict(kernel=dname, bound="mfma", achieved=flops / avg_s / 1e12, peak=PEAK_F16_TFLOPS, unit="TFLOP/s",
-                    frac=flops / avg_s / 1e12 / PEAK_F16_TFLOPS, traffic=None,
+                    frac=flops / avg_s / 1e12 / PEAK_F16_TFLOPS, traffic=traffic, traffic_source=tsrc,
                     per_launch=f"2*M*N*K = 2*{T}*{N_}*{K_} FLOP", avg_launch_ms=avg_s * 1e3)
     else:
         roof = dict(kernel=dname, bound="hbm", achieved=dv["bytes"] / dv["launches"] / avg_s / 1e9, peak=PEAK_HBM_GBS,
@@ -135,7 +153,7 @@ def main():
     d_ids1, d_mask1 = _hip.DeviceBuffer.from_array(ids1), _hip.DeviceBuffer.from_array(mask1)
     d_out1 = _hip.DeviceBuffer(D * 4)
     L1 = ids1.shape[1]
-    copies = [model] + [llmembed.Embedder.load(path).model() for _ in range(2)]
+    copies = [model] + ([llmembed.Embedder.load(path).model() for _ in range(2)] if args.latency_iters > 0 else [])
     ev0, ev1 = _hip.Event(), _hip.Event()
 
     def fwd1(mm):
@@ -154,25 +172,27 @@ def main():
             ts.append(ev0.elapsed_ms(ev1))
         return np.array(ts)
 
-    cold, warm = lat_events(copies), lat_events([model])
-    wall = []
-    for _ in range(args.latency_iters):
-        a = time.perf_counter()
-        fwd1(model)
-        stream.synchronize()
-        wall.append(time.perf_counter() - a)
-    wall = np.array(wall) * 1e3
-    v1 = d_out1.download((D,), np.float32)
-    assert abs(float(np.linalg.norm(v1.astype(np.float64))) - 1) < 1e-3, "config-1 output is not L2-normalised"
-    p50, p90 = float(np.percentile(cold, 50)), float(np.percentile(cold, 90))
-    w50 = float(np.percentile(warm, 50))
-    wall50 = float(np.percentile(wall, 50))
-    c1_bytes = 120487296.0  # Q8_0 weights + gathered token rows + LN params per forward
-    c1_roof = dict(bound="hbm", achieved=c1_bytes / (p50 * 1e-3) / 1e9, peak=PEAK_HBM_GBS, unit="GB/s",
-                   frac=c1_bytes / (p50 * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                   per_forward=f"{c1_bytes:.0f} B (weights read once + token rows + LN params)")
-    log(f"[bench] c1 device p50 {p50:.3f} ms p90 {p90:.3f} ms (cold MALL), warm p50 {w50:.3f} ms, "
-        f"host wall p50 {wall50:.3f} ms; HBM roofline {100 * c1_roof['frac']:.2f}%")
+    p50 = p90 = w50 = wall50 = c1_roof = None
+    if args.latency_iters > 0:  # --latency-iters 0 (profiling runs): config 4 only
+        cold, warm = lat_events(copies), lat_events([model])
+        wall = []
+        for _ in range(args.latency_iters):
+            a = time.perf_counter()
+            fwd1(model)
+            stream.synchronize()
+            wall.append(time.perf_counter() - a)
+        wall = np.array(wall) * 1e3
+        v1 = d_out1.download((D,), np.float32)
+        assert abs(float(np.linalg.norm(v1.astype(np.float64))) - 1) < 1e-3, "config-1 output is not L2-normalised"
+        p50, p90 = float(np.percentile(cold, 50)), float(np.percentile(cold, 90))
+        w50 = float(np.percentile(warm, 50))
+        wall50 = float(np.percentile(wall, 50))
+        c1_bytes = 120487296.0  # Q8_0 weights + gathered token rows + LN params per forward
+        c1_roof = dict(bound="hbm", achieved=c1_bytes / (p50 * 1e-3) / 1e9, peak=PEAK_HBM_GBS, unit="GB/s",
+                       frac=c1_bytes / (p50 * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                       per_forward=f"{c1_bytes:.0f} B (weights read once + token rows + LN params)")
+        log(f"[bench] c1 device p50 {p50:.3f} ms p90 {p90:.3f} ms (cold MALL), warm p50 {w50:.3f} ms, "
+            f"host wall p50 {wall50:.3f} ms; HBM roofline {100 * c1_roof['frac']:.2f}%")
     del copies
 
     # ---------------------------------------------------------------- CPU baseline
@@ -228,6 +248,7 @@ def main():
         "gpu_vs_cpu": (value / cpu["value"]) if cpu else None,
     }
     print(json.dumps(res), flush=True)
+
 
 
 if __name__ == "__main__":

@@ -45,11 +45,14 @@ struct GemmP {
   float* part;  // split-K partials [K/kchunk][M][N]
 };
 
-// GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42).
+// GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42). The quotient
+// uses the hardware reciprocal (v_rcp_f32, 1 ulp) instead of a correctly rounded division: the
+// division sequence was a third of the up/gate GEMM's epilogue, and the result is rounded to
+// f16 right after (2^-11), so the difference (~2^-23 relative in tanh) almost never shows.
 __device__ __forceinline__ float gelu_r(float v) {
   const float t = 0.7978845608f * v * (1.0f + 0.044715f * v * v);
   const float t2 = t * t;
-  float th = t * (27.0f + t2) / (27.0f + 9.0f * t2);
+  float th = t * (27.0f + t2) * __builtin_amdgcn_rcpf(27.0f + 9.0f * t2);
   if (t > 4.97f) th = 1.0f;
   else if (t < -4.97f) th = -1.0f;
   return 0.5f * v * (1.0f + th);
@@ -170,19 +173,28 @@ __global__ __launch_bounds__(WM * WN * 64, 512 / (WM * WN * 64)) void gemm_big(G
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  if constexpr (BN < 256) {
-    // XCD-aware tile order: the dispatcher deals workgroups to the 8 XCDs round-robin
-    // (workgroup b runs on XCD b % 8), so give each XCD a contiguous run of tiles, N-fastest:
-    // the feature tiles that share one token tile's X then hit the same XCD's L2 (measured:
-    // 3.5x less L2-miss traffic at N = 2304). Not for the 256-wide tiles of N = 6144: there the
-    // weights of all feature tiles overflow an XCD's L2, while the plain round-robin deal keeps
-    // each XCD on the same three feature tiles. Any bijection is correct; this is only locality.
-    const int nt = gridDim.x, G = gridDim.x * gridDim.y;
+  {
+    // XCD-aware tile order. The dispatcher deals workgroups to the 8 XCDs round-robin
+    // (workgroup b runs on XCD b % 8); each XCD has its own L2. The XCDs form an MG x NG grid
+    // over the tile grid and walk their share N-fastest, so the feature tiles that share a
+    // token tile's X run on one XCD while each XCD's weight tiles stay resident in its L2:
+    // 128-wide tiles (N <= 2304: every weight tile fits) use MG = 8, NG = 1; the 256-wide tiles
+    // of N = 6144 use MG = 4, NG = 2 (12 weight tiles, 2.5 MB per XCD). Any bijection is
+    // correct; this is only cache locality.
+    constexpr int NG = BN >= 256 ? 2 : 1, MG = 8 / NG;
+    const int nt = gridDim.x, mt = gridDim.y, G = nt * mt;
     const int b = blockIdx.x + blockIdx.y * nt, xcd = b & 7, slot = b >> 3;
-    const int q = G >> 3, r = G & 7;
-    const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-    n0 = (t % nt) * BN;
-    m0 = (t / nt) * BM;
+    if (nt % NG == 0 && mt % MG == 0) {
+      const int ntl = nt / NG, mtl = mt / MG;
+      n0 = ((xcd % NG) * ntl + slot % ntl) * BN;
+      m0 = ((xcd / NG) * mtl + slot / ntl) * BM;
+    } else if (NG == 1) {
+      // contiguous runs of the N-fastest tile order, the first G % 8 XCDs one tile longer
+      const int q = G >> 3, r = G & 7;
+      const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+      n0 = (t % nt) * BN;
+      m0 = (t / nt) * BM;
+    }
   }
   const int M = p.M, K = p.K;
   const int KT = K / KSTEP;
