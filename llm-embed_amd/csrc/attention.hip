@@ -4,8 +4,9 @@
 // (internal/ggml/ops_simd.go:46-97):
 //   s = (q . k) * 1/sqrt(64);  mask[key] == 0  ->  s = -1e9 (assigned);
 //   m = max s;  e = (s - m < -10) ? 0 : exp(s - m);  p = e / sum e;  o = sum p v.
-// One block = 64 queries of one (sequence, head); 4 waves x 16 queries. Keys stream through
-// LDS 64 at a time; S = K Q^T and O^T = V^T P^T run on v_mfma_f32_16x16x32_f16.
+// One block = 128 queries (64 when L <= 64) of one (sequence, head); one wave per 16 queries.
+// Keys stream through LDS 64 at a time; S = K Q^T and O^T = V^T P^T run on
+// v_mfma_f32_16x16x32_f16.
 //
 // Cutoff with an online max: a key is kept when s - m_run >= -10, with m_run the running max.
 // Every key the reference keeps is kept (m_run <= m_final). A kept key the reference would drop
@@ -70,10 +71,15 @@ __device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const 
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 sK[AK][HD + APAD];   // [key][dim]
-  __shared__ __attribute__((aligned(16))) _Float16 sV[HD][AK + APAD];   // [dim][key]
-  __shared__ int sMask[AK];
+// NW waves per block (16 queries each). K / V^T tiles are double-buffered: the global loads of
+// key tile kt+1 are issued before tile kt's MFMAs and land in the other LDS buffer afterwards.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
+  constexpr int NT = NW * 64, AQB = NW * 16;
+  constexpr int CPT = (AK * HD / 8) / NT;  // 16-byte chunks of each tile per thread
+  __shared__ __attribute__((aligned(16))) _Float16 sK[2][AK][HD + APAD];   // [key][dim]
+  __shared__ __attribute__((aligned(16))) _Float16 sV[2][HD][AK + APAD];   // [dim][key]
+  __shared__ int sMask[2][AK];
   __shared__ int sRedo;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -81,7 +87,10 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int L = a.L, Lp = a.Lp, H = a.H;
   const size_t head = (size_t)b * H + h;
-  const int q = qt * AQ + wave * 16 + lr;
+  const int q = qt * AQB + wave * 16 + lr;
+  // only valid (mask 1) queries may ask for the fixed-max pass: padding queries' outputs are
+  // never used, and the pass decision must not depend on how a sequence was padded
+  const bool qvalid = q < L && a.mask[(size_t)b * L + q] == 1;
 
   // Q^T fragments (B operand of S): query q, dims ks*32 + 8g .. +7
   half8 qf[2];
@@ -100,6 +109,40 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   float m_run = -INFINITY, lsum = 0.f, smin = INFINITY;
   floatx4 o[4];
 
+  uint4 kreg[CPT], vreg[CPT];
+  int mreg = 0;
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+      const int c = tid + i * NT, row = c >> 3, ch = c & 7;
+      const int key = kt * AK + row;
+      kreg[i] = key < L ? *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8) : uint4{0, 0, 0, 0};
+      const int k0 = kt * AK + ch * 8;
+      uint4 vv = uint4{0, 0, 0, 0};
+      if (k0 < L) {
+        vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
+        if (k0 + 8 > L) {
+          _Float16* e = (_Float16*)&vv;
+          for (int j = L - k0; j < 8; j++) e[j] = (_Float16)0.f;
+        }
+      }
+      vreg[i] = vv;
+    }
+    if (tid < AK) {
+      const int key = kt * AK + tid;
+      mreg = key < L ? a.mask[(size_t)b * L + key] : 0;
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+      const int c = tid + i * NT, row = c >> 3, ch = c & 7;
+      *(uint4*)&sK[buf][row][ch * 8] = kreg[i];
+      *(uint4*)&sV[buf][row][ch * 8] = vreg[i];
+    }
+    if (tid < AK) sMask[buf][tid] = mreg;
+  };
+
   if (tid == 0) sRedo = 0;
   for (int pass = 0; pass < 2; pass++) {
     const bool fixed = pass == 1;
@@ -113,32 +156,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     smin = INFINITY;
     const float m_fix = m_run;
 
+    __syncthreads();  // the buffers of a previous pass are no longer read
+    gload(t0);
+    sstore(0);
+    __syncthreads();
     for (int kt = t0; kt < t1; kt++) {
-      __syncthreads();
-      // K tile: 64 keys x 64 dims, and V^T tile: 64 dims x 64 keys
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const int c = tid + i * 256, row = c >> 3, ch = c & 7;
-        const int key = kt * AK + row;
-        uint4 kv = uint4{0, 0, 0, 0};
-        if (key < L) kv = *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8);
-        *(uint4*)&sK[row][ch * 8] = kv;
-        const int k0 = kt * AK + ch * 8;
-        uint4 vv = uint4{0, 0, 0, 0};
-        if (k0 < L) {
-          vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
-          if (k0 + 8 > L) {
-            _Float16* e = (_Float16*)&vv;
-            for (int j = L - k0; j < 8; j++) e[j] = (_Float16)0.f;
-          }
-        }
-        *(uint4*)&sV[row][ch * 8] = vv;
-      }
-      if (tid < AK) {
-        const int key = kt * AK + tid;
-        sMask[tid] = key < L ? a.mask[(size_t)b * L + key] : 0;
-      }
-      __syncthreads();
+      const int buf = (kt - t0) & 1;
+      const bool more = kt + 1 < t1;
+      if (more) gload(kt + 1);
 
       // S^T tiles: st[t][r] = score of key kidx(t, r) for query q
       floatx4 st[4];
@@ -148,7 +173,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
-          const half8 kf = *(const half8*)&sK[krow][ks * 32 + g * 8];
+          const half8 kf = *(const half8*)&sK[buf][krow][ks * 32 + g * 8];
           acc = mfma16(kf, qf[ks], acc);
         }
         st[t] = acc;
@@ -161,7 +186,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         for (int r = 0; r < 4; r++) {
           const int kl = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;
           float v = st[t][r] * scale;
-          if (sMask[kl] == 0) v = -1e9f;  // masked (and out-of-range) keys
+          if (sMask[buf][kl] == 0) v = -1e9f;  // masked (and out-of-range) keys
           s[4 * t + r] = v;
           tmax = fmaxf(tmax, v);
         }
@@ -203,15 +228,17 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
-          const half8 vf = *(const half8*)&sV[dt * 16 + lr][32 * j + 8 * g];
+          const half8 vf = *(const half8*)&sV[buf][dt * 16 + lr][32 * j + 8 * g];
           o[dt] = mfma16(vf, pf, o[dt]);
         }
       }
+      if (more) sstore(buf ^ 1);  // buffer buf^1 was last read in iteration kt-1
+      __syncthreads();
     }
     if (!fixed) {
       float sm = fminf(smin, __shfl_xor(smin, 16));
       sm = fminf(sm, __shfl_xor(sm, 32));
-      const bool flag = (q < L) && (sm - m_run < -10.f);
+      const bool flag = qvalid && (sm - m_run < -10.f);
       if (__any(flag)) sRedo = 1;  // benign race: every writer stores 1
     }
   }
@@ -234,8 +261,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
-  dim3 grid((a.L + AQ - 1) / AQ, a.H, a.B);
-  hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, st, a);
+  // 128-query blocks read each key tile once per 128 queries; short sequences keep 64
+  if (a.L > 64) {
+    const dim3 grid((a.L + 127) / 128, a.H, a.B);
+    hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(512), 0, st, a);
+  } else {
+    const dim3 grid(1, a.H, a.B);
+    hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 
