@@ -54,6 +54,8 @@ def main():
     ap.add_argument("--latency-iters", type=int, default=200)
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--mix", default="Q8_0")
+    ap.add_argument("--no-extras", dest="extras", action="store_false",
+                    help="skip the config-3 / config-5 / other-quantisation runs")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="for rocprofv3 --pmc runs: two config-4 forwards, then one 256 MiB device-to-device copy "
                          "(the calibration of FETCH_SIZE / WRITE_SIZE); prints no JSON")
@@ -195,6 +197,54 @@ def main():
             f"host wall p50 {wall50:.3f} ms; HBM roofline {100 * c1_roof['frac']:.2f}%")
     del copies
 
+    # ---------------------------------------------------------------- other configs
+    # Config 4 on Q6_K and Q5_K_M weights, config 3 (B=64, lengths U[16,128] padded to 128,
+    # Q4_K_M) and config 5 (B=8, lengths U[1024,2048] padded to 2048, Q8_0): throughput over
+    # valid sequences, per-kernel shares, and config 5's attention share and HBM rate.
+    extras = {}
+    if args.extras:
+        def run_cfg(cfg, mix, steps):
+            ids_c, mask_c = synth.config_inputs(cfg)
+            Bc, Lc = ids_c.shape
+            mm = llmembed.Embedder.load(synth.model_path(spec, mix, synth.CONFIG_SEED + cfg)).model()
+            di, dm = _hip.DeviceBuffer.from_array(ids_c), _hip.DeviceBuffer.from_array(mask_c)
+            do = _hip.DeviceBuffer(Bc * D * 4)
+
+            def st_():
+                check(L_.lle_embed_batch_async(mm.h, di.ptr, dm.ptr, Bc, Lc, D, do.ptr, stream.h))
+
+            st_()
+            _hip.synchronize()
+            mm.set_timing(True)
+            t_a = time.perf_counter()
+            for _ in range(steps):
+                st_()
+            _hip.synchronize()
+            t_b = time.perf_counter()
+            kt_c = mm.timing()
+            mm.set_timing(False)
+            o_c = do.download((Bc, D), np.float32)
+            assert np.all(np.isfinite(o_c)), f"config {cfg} {mix}: non-finite output"
+            tot_ms = sum(v["total_ms"] for v in kt_c.values())
+            ms = 1000.0 * (t_b - t_a) / steps
+            r = dict(mix=mix, batch=int(Bc), seq_len=int(Lc), valid_tokens=int(mask_c.sum()),
+                     emb_per_s=Bc * steps / (t_b - t_a), ms_per_step=ms,
+                     shares={k: round(v["total_ms"] / tot_ms, 4) for k, v in kt_c.items()})
+            if "attention" in kt_c:
+                at = kt_c["attention"]
+                r["attention_share"] = at["total_ms"] / tot_ms
+                r["attention_algorithmic_gbs"] = at["bytes"] / (at["total_ms"] * 1e-3) / 1e9
+            log(f"[bench] config {cfg} {mix}: {r['emb_per_s']:.1f} emb/s, {ms:.3f} ms/step"
+                + (f", attention {100 * r['attention_share']:.1f}% of kernel time at {r['attention_algorithmic_gbs']:.0f} GB/s (Q,K,V,O bytes)"
+                   if "attention_share" in r else ""))
+            mm.close()
+            return r
+
+        extras["config4_Q6_K"] = run_cfg(4, "Q6_K", 5)
+        extras["config4_Q5_K_M"] = run_cfg(4, "Q5_K_M", 5)
+        extras["config3_Q4_K_M"] = run_cfg(3, "Q4_K_M", 10)
+        extras["config5_Q8_0"] = run_cfg(5, "Q8_0", 5)
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if args.cpu_seqs > 0:
@@ -246,6 +296,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "gpu_vs_cpu": (value / cpu["value"]) if cpu else None,
+        "other_configs": extras,
     }
     print(json.dumps(res), flush=True)
 

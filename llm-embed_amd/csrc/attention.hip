@@ -80,6 +80,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 sK[2][AK][HD + APAD];   // [key][dim]
   __shared__ __attribute__((aligned(16))) _Float16 sV[2][HD][AK + APAD];   // [dim][key]
   __shared__ int sMask[2][AK];
+  __shared__ int sFull[2];
   __shared__ int sRedo;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -104,6 +105,16 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
 
   const int klo = a.kv_range[2 * b], khi = a.kv_range[2 * b + 1];
   const int t0 = klo / AK, t1 = (khi + AK - 1) / AK;
+  if (qt * AQB >= khi) {
+    // every query of this block lies past the last valid key, so it is padding (mask 0):
+    // its output is never used, but stays finite (zero) for the next layer's masked P.V
+    if (q < L) {
+      __half* dst = a.out + ((size_t)b * L + q) * a.D + h * HD + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) *(uint2*)(dst + dt * 16) = uint2{0u, 0u};
+    }
+    return;
+  }
   const float scale = 0.125f;  // float32(1/sqrt(64)), bert.go:362
 
   float m_run = -INFINITY, lsum = 0.f, smin = INFINITY;
@@ -121,9 +132,12 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
       uint4 vv = uint4{0, 0, 0, 0};
       if (k0 < L) {
         vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
-        if (k0 + 8 > L) {
-          _Float16* e = (_Float16*)&vv;
-          for (int j = L - k0; j < 8; j++) e[j] = (_Float16)0.f;
+        if (k0 + 8 > L) {  // zero the keys at and past L (the buffer's padding columns)
+          const int nv = L - k0;
+          vv.x &= (nv > 0 ? 0xFFFFu : 0u) | (nv > 1 ? 0xFFFF0000u : 0u);
+          vv.y &= (nv > 2 ? 0xFFFFu : 0u) | (nv > 3 ? 0xFFFF0000u : 0u);
+          vv.z &= (nv > 4 ? 0xFFFFu : 0u) | (nv > 5 ? 0xFFFF0000u : 0u);
+          vv.w &= (nv > 6 ? 0xFFFFu : 0u) | (nv > 7 ? 0xFFFF0000u : 0u);
         }
       }
       vreg[i] = vv;
@@ -141,6 +155,10 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
       *(uint4*)&sV[buf][row][ch * 8] = vreg[i];
     }
     if (tid < AK) sMask[buf][tid] = mreg;
+    if (tid < 64) {  // wave 0: one flag per tile, set when all 64 keys are valid
+      const bool all = __all(mreg == 1);
+      if (tid == 0) sFull[buf] = all;
+    }
   };
 
   if (tid == 0) sRedo = 0;
@@ -179,17 +197,20 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
         st[t] = acc;
       }
       float s[16];
-      float tmax = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int kl = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;
-          float v = st[t][r] * scale;
-          if (sMask[buf][kl] == 0) v = -1e9f;  // masked (and out-of-range) keys
-          s[4 * t + r] = v;
-          tmax = fmaxf(tmax, v);
-        }
+        for (int r = 0; r < 4; r++) s[4 * t + r] = st[t][r] * scale;
+      if (!sFull[buf]) {  // masked (and out-of-range) keys; tiles of valid keys skip the lookups
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            if (sMask[buf][32 * (t >> 1) + 8 * g + 4 * (t & 1) + r] == 0) s[4 * t + r] = -1e9f;
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, s[i]);
       float alpha = 1.f, mref;
       if (!fixed) {
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
@@ -204,14 +225,12 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
       float e[16];
       float ps = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
+      for (int i = 0; i < 16; i++) {  // branch-free: exp of a dropped key (z < -10) is discarded
         const float z = s[i] - mref;
-        if (z < -10.f) {
-          e[i] = 0.f;
-        } else {
-          e[i] = __expf(z);
-          smin = fminf(smin, s[i]);
-        }
+        const bool keep = z >= -10.f;
+        const float ex = __expf(z);
+        e[i] = keep ? ex : 0.f;
+        smin = keep ? fminf(smin, s[i]) : smin;
         ps += e[i];
       }
       lsum = lsum * alpha + ps;
