@@ -224,6 +224,56 @@ __device__ __forceinline__ void decode_seg_h(const RawSeg& r, int k0, uint4& lo,
     }
     lo = uint4{o[0], o[1], o[2], o[3]};
     hi = uint4{o[4], o[5], o[6], o[7]};
+  } else if constexpr (FMT == 12 || FMT == 13 || FMT == 14) {
+    // K-quants: the codes as bytes of four words, converted by byte (v_cvt_f32_ubyte*), one fma
+    // per value with the same single rounding as decode_seg (the products are exact), packed
+    // with round-to-nearest-even. Scale bytes are picked out of the header words by shifts.
+    const int s = (k0 >> 4) & 3, hn = s >> 1;  // hn: high nibbles of the code bytes
+    uint32_t qb[4];  // byte i of word w = code of element 4w + i
+    float ds, off;   // value = fma(ds, code, off); Q6_K: ds * (code + off)
+    if constexpr (FMT == 14) {
+      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.y >> 16));
+      ds = d * (float)(int8_t)(r.y & 0xff);
+      off = -32.0f;  // value = ds * (code - 32): subtract first, so code 32 gives ds * +0 (-0 for ds < 0)
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        const uint32_t nib = hn ? (u4_word(r.q, w) >> 4) & 0x0F0F0F0Fu : u4_word(r.q, w) & 0x0F0F0F0Fu;
+        const uint32_t t = (r.x >> (8 * w)) & 0xffu;  // four 2-bit high parts
+        const uint32_t h2 = ((t << 4) | (t << 10) | (t << 16) | (t << 22)) & 0x30303030u;
+        qb[w] = nib | h2;
+      }
+    } else {
+      const int g = k0 >> 6, j = 2 * (g & 3) + hn, sh = 8 * (j & 3);
+      const uint32_t y = (r.hdr.y >> sh) & 0xffu, z = (r.hdr.z >> sh) & 0xffu, w3 = (r.hdr.w >> sh) & 0xffu;
+      const uint32_t sc = j < 4 ? (y & 63u) : ((w3 & 0xFu) | ((y >> 6) << 4));
+      const uint32_t m = j < 4 ? (z & 63u) : ((w3 >> 4) | ((z >> 6) << 4));
+      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr.x & 0xffffu));
+      const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr.x >> 16));
+      ds = d * (float)sc;
+      off = -(dmin * (float)m);
+      const uint32_t qh16 = FMT == 13 ? (r.x >> (16 * (s & 1))) & 0xffffu : 0u;
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        uint32_t nib = hn ? (u4_word(r.q, w) >> 4) & 0x0F0F0F0Fu : u4_word(r.q, w) & 0x0F0F0F0Fu;
+        if constexpr (FMT == 13)  // bit i of the 4-bit group -> bit 4 of byte i (no carries)
+          nib |= (((qh16 >> (4 * w)) & 0xFu) * 0x00204081u & 0x01010101u) << 4;
+        qb[w] = nib;
+      }
+    }
+    auto val = [&](uint32_t code) {
+      if constexpr (FMT == 14)
+        return ds * ((float)code + off);  // exact, as (d*sc)*(q-32) in the reference
+      else
+        return fmaf(ds, (float)code, off);
+    };
+    uint32_t o[8];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      o[2 * w] = pack_rn(val(qb[w] & 0xffu), val((qb[w] >> 8) & 0xffu));
+      o[2 * w + 1] = pack_rn(val((qb[w] >> 16) & 0xffu), val(qb[w] >> 24));
+    }
+    lo = uint4{o[0], o[1], o[2], o[3]};
+    hi = uint4{o[4], o[5], o[6], o[7]};
   } else {
     float v[16];
     decode_seg<FMT>(r, k0, v);
