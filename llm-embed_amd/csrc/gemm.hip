@@ -43,6 +43,7 @@ struct GemmP {
   int L, Lp, H, D;
   __half* g;
   float* part;  // split-K partials [K/kchunk][M][N]
+  const __half* w16;  // resident f16 copy of the weights [N][K], or null
 };
 
 // GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42). The quotient
@@ -412,6 +413,200 @@ __global__ __launch_bounds__(WM * WN * 64, 512 / (WM * WN * 64)) void gemm_big(G
 }
 
 // ---------------------------------------------------------------------------------------
+// Large-M GEMM on the resident f16 copy of the weights (RNE of the dequantisation, made once at
+// upload, as the reference's PreDequant does in f32): both operands are plain f16, so both tiles
+// go global -> LDS by buffer_load ... lds (LDS-DMA: no VGPR staging, no ds_write, no VALU), and
+// the loads of K step kt+1 fly while step kt's MFMAs run. LDS layout, fragment reads, MFMA
+// sequence, chunk totals and epilogue are gemm_big's, so every output bit is the same.
+// One LDS-DMA instruction moves 1 KB = 8 tile rows; lane L fills slot L % 8 of row L / 8, so it
+// fetches the logical 16-byte chunk (L % 8) ^ (row & 7) (the XOR swizzle applied on the load).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane from the buffer into LDS at lds + 16 * lane (one 1-KB row group per wave).
+// Written as inline assembly: the compiler's wait-count pass tracks at most a few LDS-DMA
+// stores and otherwise waits for all of them before every LDS read, which would serialise a
+// multi-stage pipeline. The kernel orders these loads itself (s_waitcnt vmcnt + s_barrier).
+typedef unsigned int u32x4_sgpr __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void dma16(u32x4_sgpr r, void* lds, int voff, int soff) {
+  const uint32_t base = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(base), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+}
+// Buffer descriptor as four SGPRs: base, stride 0, num_records = 2^32 - 1, default format.
+__device__ __forceinline__ u32x4_sgpr rsrc_words(const void* p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  return u32x4_sgpr{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, 0xffffffffu, 0x00020000u};
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool MULTI>
+__global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN, FB = TN / 16, TB = TM / 16;
+  constexpr int XI = BM / 8 / NW, WI = BN / 8 / NW;  // 1-KB loads per wave per K step
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows per wave");
+  static_assert(NS == 2 || NS == 3, "stages");
+  // one LDS object per stage: the compiler's wait-count pass then knows that reading one stage
+  // does not depend on the LDS-DMA loads still flying into another
+  __shared__ __attribute__((aligned(1024))) _Float16 sW0[BN][KSTEP], sW1[BN][KSTEP], sW2[NS > 2 ? BN : 1][KSTEP];
+  __shared__ __attribute__((aligned(1024))) _Float16 sX0[BM][KSTEP], sX1[BM][KSTEP], sX2[NS > 2 ? BM : 1][KSTEP];
+  auto stW = [&](auto S) -> _Float16(*)[KSTEP] {
+    if constexpr (decltype(S)::value == 0) return sW0;
+    else if constexpr (decltype(S)::value == 1) return sW1;
+    else return sW2;
+  };
+  auto stX = [&](auto S) -> _Float16(*)[KSTEP] {
+    if constexpr (decltype(S)::value == 0) return sX0;
+    else if constexpr (decltype(S)::value == 1) return sX1;
+    else return sX2;
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  {
+    // the same XCD-aware tile order as gemm_big
+    constexpr int NG = BN >= 256 ? 2 : 1, MG = 8 / NG;
+    const int nt = gridDim.x, mt = gridDim.y, G = nt * mt;
+    const int b = blockIdx.x + blockIdx.y * nt, xcd = b & 7, slot = b >> 3;
+    if (nt % NG == 0 && mt % MG == 0) {
+      const int ntl = nt / NG, mtl = mt / MG;
+      n0 = ((xcd % NG) * ntl + slot % ntl) * BN;
+      m0 = ((xcd / NG) * mtl + slot / ntl) * BM;
+    } else if (NG == 1) {
+      const int q = G >> 3, r = G & 7;
+      const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+      n0 = (t % nt) * BN;
+      m0 = (t / nt) * BM;
+    }
+  }
+  const int M = p.M, K = p.K;
+  const int KT = K / KSTEP;
+  const int steps_per_chunk = kchunk_of(K) / KSTEP;
+
+  floatx4 acc[FB][TB];
+  floatx4 tot[MULTI ? FB : 1][MULTI ? TB : 1];
+#pragma unroll
+  for (int i = 0; i < FB; i++)
+#pragma unroll
+    for (int j = 0; j < TB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (MULTI) {
+#pragma unroll
+    for (int i = 0; i < FB; i++)
+#pragma unroll
+      for (int j = 0; j < TB; j++) tot[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // loop-invariant byte offsets; the K step advances in the scalar offset. Rows past M re-read
+  // row M-1 (they only feed output rows that are never stored).
+  const u32x4_sgpr rx = rsrc_words(p.x), rw = rsrc_words(p.w16);
+  int xo[XI], wo[WI];
+#pragma unroll
+  for (int j = 0; j < XI; j++) {
+    const int r = (wave + j * NW) * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    xo[j] = (min(m0 + r, M - 1) * K + c * 8) * 2;
+  }
+#pragma unroll
+  for (int j = 0; j < WI; j++) {
+    const int r = (wave + j * NW) * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    wo[j] = ((n0 + r) * K + c * 8) * 2;
+  }
+  auto issue = [&](auto S, int kt) {
+    _Float16(*sx)[KSTEP] = stX(S);
+    _Float16(*sw)[KSTEP] = stW(S);
+#pragma unroll
+    for (int j = 0; j < XI; j++) dma16(rx, &sx[(wave + j * NW) * 8][0], xo[j], kt * KSTEP * 2);
+#pragma unroll
+    for (int j = 0; j < WI; j++) dma16(rw, &sw[(wave + j * NW) * 8][0], wo[j], kt * KSTEP * 2);
+  };
+  const int lr = lane & 15, lg = lane >> 4;
+  auto compute = [&](auto S, int kt) {
+    const _Float16(*sw)[KSTEP] = stW(S);
+    const _Float16(*sx)[KSTEP] = stX(S);
+    half8 af[2][FB], bf[2][TB];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+      for (int i = 0; i < FB; i++) af[ks][i] = *(const half8*)&sw[wn * TN + i * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+#pragma unroll
+      for (int j = 0; j < TB; j++) bf[ks][j] = *(const half8*)&sx[wm * TM + j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (int i = 0; i < FB; i++)
+#pragma unroll
+        for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[ks][i], bf[ks][j], acc[i][j]);
+    if constexpr (MULTI) {
+      if ((kt + 1) % steps_per_chunk == 0) {
+#pragma unroll
+        for (int i = 0; i < FB; i++)
+#pragma unroll
+          for (int j = 0; j < TB; j++) {
+            tot[i][j] += acc[i][j];
+            acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+          }
+      }
+    }
+  };
+  // NS LDS stages, loads issued NS-1 K steps ahead (KT % NS == 0). At the top of step kt each
+  // wave waits until only the loads of the NS-2 younger steps are in flight (its step-kt loads
+  // have landed) and its LDS reads are done; the barrier then makes every wave's step-kt data
+  // visible and frees the stage of step kt-1 for the loads of step kt+NS-1. s_barrier is used
+  // bare (with compiler-only fences): __syncthreads() would also wait for every load in flight.
+  constexpr int PER_STEP = XI + WI;  // LDS-DMA instructions per wave per K step
+  constexpr int VM = (NS - 2) * PER_STEP;
+  static_assert(VM < 64, "vmcnt range");
+  constexpr int WAIT = (VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4);  // vmcnt(VM) lgkmcnt(0)
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  auto step = [&](auto S, auto SN, int kt) {  // SN: the stage of step kt + NS - 1
+    if (kt + NS - 2 < KT)
+      __builtin_amdgcn_s_waitcnt(WAIT);
+    else
+      __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + NS - 1 < KT) issue(SN, kt + NS - 1);
+    compute(S, kt);
+  };
+  issue(S0{}, 0);
+  if constexpr (NS == 3) issue(S1{}, 1);
+  for (int kt = 0; kt < KT; kt += NS) {
+    if constexpr (NS == 2) {
+      step(S0{}, S1{}, kt);
+      step(S1{}, S0{}, kt + 1);
+    } else {
+      step(S0{}, S2{}, kt);
+      step(S1{}, S0{}, kt + 1);
+      step(S2{}, S1{}, kt + 2);
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < TB; j++) {
+    const int m = m0 + wm * TM + j * 16 + lr;
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < FB; i++) {
+        floatx4 v;
+        if constexpr (MULTI) {
+          v = tot[i][j];
+        } else {
+          v = floatx4{0.f, 0.f, 0.f, 0.f};
+          v += acc[i][j];  // total = 0 + chunk, as the split-K reduction computes it
+        }
+        epilogue<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Full-row GEMM + residual + LayerNorm (h = LN(h + X W^T)) for N = 768: one block owns BM
 // complete rows, so the LayerNorm runs in the epilogue instead of a second pass over h.
 // 8 waves, each 96 features x BM tokens (6 x BM/16 MFMA tiles). K steps of 32 (one MFMA deep):
@@ -733,6 +928,21 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
     return launch_small<FMT, 64, EPI>(p, st, reduce);
   }
   const bool multi = p.K > kchunk_of(p.K);
+  if (p.M >= 1024 && p.w16) {
+    if (!multi && p.N >= 4096 && p.N % 256 == 0) {  // 2 stages of 64 KB
+      dim3 grid(p.N / 256, (p.M + 255) / 256);
+      hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
+      return hipGetLastError();
+    }
+    if ((p.K / KSTEP) % 3 == 0) {
+      dim3 grid(p.N / 128, (p.M + 255) / 256);  // 3 stages of 48 KB
+      if (multi)
+        hipLaunchKernelGGL((gemm_h<256, 128, 4, 2, 3, EPI, true>), grid, dim3(512), 0, st, p);
+      else
+        hipLaunchKernelGGL((gemm_h<256, 128, 4, 2, 3, EPI, false>), grid, dim3(512), 0, st, p);
+      return hipGetLastError();
+    }
+  }
   if (p.M >= 1024) {
     if (!multi && p.N >= 4096 && p.N % 256 == 0) {
       // 256 x 256 tiles: each X tile is read by half as many blocks, each decoded weight feeds
@@ -787,6 +997,7 @@ static GemmP make_params(const GemmArgs& a) {
   p.D = a.d_model;
   p.g = a.g;
   p.part = a.part;
+  p.w16 = a.w->w16;
   return p;
 }
 

@@ -45,6 +45,8 @@ struct WeightDev {
   const uint8_t* p1 = nullptr;  // scales / hdr / qh
   const uint8_t* p2 = nullptr;  // qh (Q5_K) / sc (Q6_K)
   const uint8_t* p3 = nullptr;  // d (Q6_K)
+  // resident f16 copy [N][K] (RNE of the dequantisation) for the large-M GEMMs, or null
+  __half* w16 = nullptr;
 };
 
 // Host-side re-layout of GGUF blocks of a [N][K] matrix into the planes above.

@@ -423,6 +423,23 @@ static int upload_weight(int device, int type, const uint8_t* gguf, int K, int N
   wd->p1 = b + off[1];
   wd->p2 = b + off[2];
   wd->p3 = b + off[3];
+  // Resident f16 copy [N][K] for the large-M GEMMs: the MFMA operand (RNE of the dequantised
+  // value), made once here as the reference's PreDequant makes its f32 copy at load
+  // (internal/embed/bert.go:542-576). Without memory for it the GEMMs decode on the fly.
+  void* h = nullptr;
+  if (hipMalloc(&h, (size_t)N * K * 2) == hipSuccess) {
+    hipError_t e2 = launch_dequant_weight_h(*wd, (uint16_t*)h, nullptr);
+    if (e2 == hipSuccess) e2 = hipStreamSynchronize(nullptr);
+    if (e2 != hipSuccess) {
+      (void)hipFree(h);
+      if (!allocs) (void)hipFree(d);  // a model frees its allocs list itself
+      return fail(LLE_EDEVICE, std::string("weight f16 copy: ") + hipGetErrorString(e2));
+    }
+    if (allocs) allocs->push_back(h);
+    wd->w16 = (__half*)h;
+  } else {
+    (void)hipGetLastError();
+  }
   (void)device;
   return LLE_OK;
 }
@@ -786,6 +803,7 @@ int32_t lle_weight_create(int32_t type, const void* blocks, int32_t K, int32_t N
   }
   if (hipStreamCreate(&w->stream) != hipSuccess) {
     (void)hipFree(w->w.base);
+    if (w->w.w16) (void)hipFree(w->w.w16);
     delete w;
     return fail(LLE_EDEVICE, "hipStreamCreate");
   }
@@ -798,6 +816,7 @@ int32_t lle_weight_destroy(lle_weight* w) {
   (void)hipSetDevice(w->device);
   (void)hipStreamSynchronize(w->stream);
   (void)hipFree(w->w.base);
+  if (w->w.w16) (void)hipFree(w->w.w16);
   (void)hipStreamDestroy(w->stream);
   delete w;
   return LLE_OK;
