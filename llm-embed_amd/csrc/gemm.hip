@@ -619,6 +619,51 @@ __device__ __forceinline__ int swr(int row) { return ((row >> 1) ^ (row >> 3)) &
 
 constexpr int LN_N = 768, LN_KS = 32, LN_RS = LN_N + 4;  // LN staging row stride (floats)
 
+// Epilogue of the full-row kernels: x = h + total (the residual epilogue's add) staged per 32
+// tokens in LDS (row stride 772 floats: conflict-free), then LayerNorm by ln_row with
+// ln_kernel's element-to-lane mapping (wave w: 4 rows per half). Call after a barrier that
+// ends every read of the K-loop stages, which smem overlays.
+template <int BM>
+__device__ __forceinline__ void rowln_finish(const floatx4 (&acc)[6][BM / 16], unsigned char* smem, const GemmP& p,
+                                             const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                             float eps, __half* h16, int m0, int wn, int lane) {
+  constexpr int FB = 6, TN = 96;
+  const int lr = lane & 15, lg = lane >> 4, M = p.M;
+  float* sR = (float*)smem;
+#pragma unroll
+  for (int half = 0; half < BM / 32; half++) {
+#pragma unroll
+    for (int j = 2 * half; j < 2 * half + 2; j++) {
+      const int tl = (j - 2 * half) * 16 + lr, m = m0 + j * 16 + lr;
+#pragma unroll
+      for (int i = 0; i < FB; i++) {
+        const int f = wn * TN + i * 16 + lg * 4;
+        floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+        v += acc[i][j];  // total = 0 + chunk
+        floatx4 x = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (m < M) {
+          const floatx4 h = *(const floatx4*)(p.y + (size_t)m * LN_N + f);
+          x.x = h.x + v.x; x.y = h.y + v.y; x.z = h.z + v.z; x.w = h.w + v.w;
+        }
+        *(floatx4*)&sR[tl * LN_RS + f] = x;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int tl = wn * 4 + r, m = m0 + half * 32 + tl;
+      if (m < M) {
+        float x[MAXE];
+#pragma unroll
+        for (int i = 0; i < MAXE; i++)
+          if (i < LN_N / 64) x[i] = sR[tl * LN_RS + lane + 64 * i];
+        ln_row(x, LN_N / 64, LN_N, lnw, lnb, eps, lane, p.y + (size_t)m * LN_N, h16 + (size_t)m * LN_N);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <int FMT, int BM>
 __global__ __launch_bounds__(512, 1) void gemm_rowln(GemmP p, const float* __restrict__ lnw,
                                                      const float* __restrict__ lnb, float eps, __half* h16) {
@@ -737,41 +782,98 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln(GemmP p, const float* __res
   step(S1{}, S0{}, kt + 1, false);
   __syncthreads();  // every stage read: LDS is free for the row staging
 
-  // Epilogue: x = h + total (the residual epilogue's add) staged per 32 tokens in LDS, then
-  // LayerNorm by ln_row with ln_kernel's element-to-lane mapping (wave w: 4 rows per half).
-  float* sR = (float*)smem;
+  rowln_finish<BM>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane);
+}
+
+// The full-row kernel on the resident f16 weights: both tiles by LDS-DMA (one instruction =
+// 16 rows of 64 bytes; lane L fills slot L % 4 of row L / 4 with logical chunk (L % 4) ^ swr(row))
+// through three LDS stages of 52 KB, loads two K steps ahead; MFMA order and epilogue as above.
+template <int BM>
+__global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __restrict__ lnw,
+                                                       const float* __restrict__ lnb, float eps, __half* h16) {
+  constexpr int NS = 3, WN = 8, TN = LN_N / WN, FB = TN / 16, TB = BM / 16;
+  constexpr int W_STAGE = LN_N * LN_KS * 2, X_STAGE = BM * LN_KS * 2, STAGE = W_STAGE + X_STAGE;
+  constexpr int WG = LN_N / 16 / WN;  // weight row groups per wave per step (6)
+  constexpr int XG = BM / 16;         // X row groups per step (4): wave w loads group w % XG
+  constexpr int PER_STEP = WG + 1;    // LDS-DMA instructions per wave per step
+  constexpr int R_BYTES = 32 * LN_RS * 4;
+  constexpr int SMEM = NS * STAGE > R_BYTES ? NS * STAGE : R_BYTES;
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
+  typedef _Float16 Row[LN_KS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = blockIdx.x * BM;
+  const int M = p.M, K = p.K;
+  const int KT = K / LN_KS;
+
+  floatx4 acc[FB][TB];
 #pragma unroll
-  for (int half = 0; half < BM / 32; half++) {
+  for (int i = 0; i < FB; i++)
 #pragma unroll
-    for (int j = 2 * half; j < 2 * half + 2; j++) {
-      const int tl = (j - 2 * half) * 16 + lr, m = m0 + j * 16 + lr;
+    for (int j = 0; j < TB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const u32x4_sgpr rx = rsrc_words(p.x), rw = rsrc_words(p.w16);
+  int wo[WG];
 #pragma unroll
-      for (int i = 0; i < FB; i++) {
-        const int f = wn * TN + i * 16 + lg * 4;
-        floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
-        v += acc[i][j];  // total = 0 + chunk
-        floatx4 x = floatx4{0.f, 0.f, 0.f, 0.f};
-        if (m < M) {
-          const floatx4 h = *(const floatx4*)(p.y + (size_t)m * LN_N + f);
-          x.x = h.x + v.x; x.y = h.y + v.y; x.z = h.z + v.z; x.w = h.w + v.w;
-        }
-        *(floatx4*)&sR[tl * LN_RS + f] = x;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int tl = wn * 4 + r, m = m0 + half * 32 + tl;
-      if (m < M) {
-        float x[MAXE];
-#pragma unroll
-        for (int i = 0; i < MAXE; i++)
-          if (i < LN_N / 64) x[i] = sR[tl * LN_RS + lane + 64 * i];
-        ln_row(x, LN_N / 64, LN_N, lnw, lnb, eps, lane, p.y + (size_t)m * LN_N, h16 + (size_t)m * LN_N);
-      }
-    }
-    __syncthreads();
+  for (int g = 0; g < WG; g++) {
+    const int r = (wn + g * WN) * 16 + (lane >> 2), c = (lane & 3) ^ swr(r);
+    wo[g] = (r * K + c * 8) * 2;
   }
+  const int xg = wn % XG;
+  int xo;
+  {
+    const int r = xg * 16 + (lane >> 2), c = (lane & 3) ^ swr(r);
+    xo = (min(m0 + r, M - 1) * K + c * 8) * 2;
+  }
+  auto stageW = [&](int s) { return (Row*)(smem + s * STAGE); };
+  auto stageX = [&](int s) { return (Row*)(smem + s * STAGE + W_STAGE); };
+  auto issue = [&](int s, int kt) {
+    Row* sw = stageW(s);
+#pragma unroll
+    for (int g = 0; g < WG; g++) dma16(rw, &sw[(wn + g * WN) * 16][0], wo[g], kt * LN_KS * 2);
+    dma16(rx, &stageX(s)[xg * 16][0], xo, kt * LN_KS * 2);  // waves w and w + 4 load the same rows
+  };
+  auto compute = [&](int s) {
+    const Row* sw = stageW(s);
+    const Row* sx = stageX(s);
+    half8 af[FB], bf[TB];
+#pragma unroll
+    for (int i = 0; i < FB; i++) {
+      const int f = wn * TN + i * 16 + lr;
+      af[i] = *(const half8*)&sw[f][(lg ^ swr(f)) * 8];
+    }
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      const int t = j * 16 + lr;
+      bf[j] = *(const half8*)&sx[t][(lg ^ swr(t)) * 8];
+    }
+#pragma unroll
+    for (int i = 0; i < FB; i++)
+#pragma unroll
+      for (int j = 0; j < TB; j++) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+  };
+  constexpr int VM = (NS - 2) * PER_STEP;
+  constexpr int WAIT = (VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4);  // vmcnt(VM) lgkmcnt(0)
+  issue(0, 0);
+  issue(1, 1);
+  int stage = 0;
+  for (int kt = 0; kt < KT; kt++) {  // as in gemm_h: wait for step kt's loads, barrier, refill
+    if (kt + NS - 2 < KT)
+      __builtin_amdgcn_s_waitcnt(WAIT);
+    else
+      __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + NS - 1 < KT) issue(stage == 0 ? NS - 1 : stage - 1, kt + NS - 1);
+    compute(stage);
+    stage = stage == NS - 1 ? 0 : stage + 1;
+  }
+  __syncthreads();  // every stage read: LDS is free for the row staging
+  rowln_finish<BM>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1021,6 +1123,13 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
   const GemmP p = make_params(a);
   const int nch = p.K / kchunk_of(p.K);
   if ((int64_t)p.M * p.K * 2 > INT32_MAX) return hipErrorInvalidValue;  // 32-bit buffer offsets
+  // Q8_0 keeps the decoding kernel: its packed decode is cheap and the block streams half the
+  // weight bytes (measured 0.114 vs 0.124 ms at 32768 tokens); the K-quants' decode is not cheap
+  if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16 && a.w->type != LLE_TYPE_Q8_0 &&
+      (p.K / LN_KS) % 3 == 0) {
+    hipLaunchKernelGGL((gemm_rowln_h<64>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16);
+    return hipGetLastError();
+  }
   if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) {
     const dim3 grid((p.M + 63) / 64), blk(512);
     switch (a.w->type) {
