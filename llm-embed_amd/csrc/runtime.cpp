@@ -8,6 +8,7 @@
 //   BertModel.Forward (internal/embed/bert.go:216-285)      ->  forward() below
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -426,8 +427,10 @@ static int upload_weight(int device, int type, const uint8_t* gguf, int K, int N
   // Resident f16 copy [N][K] for the large-M GEMMs: the MFMA operand (RNE of the dequantised
   // value), made once here as the reference's PreDequant makes its f32 copy at load
   // (internal/embed/bert.go:542-576). Without memory for it the GEMMs decode on the fly.
+  // LLE_NO_F16_COPY=1 (read per upload) skips the copy: tests use it to run the decoding path.
+  const char* nocopy = getenv("LLE_NO_F16_COPY");
   void* h = nullptr;
-  if (hipMalloc(&h, (size_t)N * K * 2) == hipSuccess) {
+  if (!(nocopy && nocopy[0] == '1') && hipMalloc(&h, (size_t)N * K * 2) == hipSuccess) {
     hipError_t e2 = launch_dequant_weight_h(*wd, (uint16_t*)h, nullptr);
     if (e2 == hipSuccess) e2 = hipStreamSynchronize(nullptr);
     if (e2 != hipSuccess) {

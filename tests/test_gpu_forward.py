@@ -98,6 +98,26 @@ def test_full_row_layernorm_path_bitexact(gpu, small_spec, mix):
     compare(batch[1], o.embed(seqs[1]), f"{mix} full-row LN")
 
 
+@pytest.mark.parametrize("mix", ["Q8_0", "Q4_K_M"])
+def test_decoding_gemm_path_matches_f16_copy_path(gpu, small_spec, mix, monkeypatch):
+    """Without the resident f16 weight copy (LLE_NO_F16_COPY=1) the >= 1024-token GEMMs decode
+    the quantised planes in their loop; the embeddings must equal the f16-copy path's bit for
+    bit (same operands, same MFMA order)."""
+    p = synth.model_path(small_spec, mix, 100, 0.02)
+    rng = np.random.default_rng(45)
+    ids = rng.integers(0, small_spec.vocab, (12, 100)).astype(np.int32)
+    mask = np.ones_like(ids)
+    mask[3, 70:] = 0
+    ref = models(small_spec, mix)[0].embed_padded(ids, mask)
+    monkeypatch.setenv("LLE_NO_F16_COPY", "1")
+    e = Embedder.load(p)
+    try:
+        got = e.embed_padded(ids, mask)
+    finally:
+        e.model().close()
+    assert np.array_equal(bits(got), bits(ref))
+
+
 def test_padded_batch_vs_oracle(gpu, small_spec):
     """Config-3 style: right-padded batch with per-row lengths, Q4_K_M."""
     e, o = models(small_spec, "Q4_K_M")
