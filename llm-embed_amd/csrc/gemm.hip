@@ -499,6 +499,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
       for (int j = 0; j < TB; j++) tot[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // The RoPE epilogue's cos/sin pairs are loaded before the K loop (their latency then hides
+  // behind it; issued after the first LDS-DMA loads would break the vmcnt accounting below,
+  // which counts on every older memory operation being complete). Rows past M load row M-1.
+  constexpr bool PRE = EPI == EPI_QKV;
+  floatx4 eop[PRE ? FB : 1][PRE ? TB : 1];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int j = 0; j < TB; j++)
+#pragma unroll
+      for (int i = 0; i < FB; i++)
+        eop[i][j] = epi_operands<EPI>(p, min(m0 + wm * TM + j * 16 + (lane & 15), M - 1),
+                                      n0 + wn * TN + i * 16 + (lane >> 4) * 4);
+  }
+
   // loop-invariant byte offsets; the K step advances in the scalar offset. Rows past M re-read
   // row M-1 (they only feed output rows that are never stored).
   const u32x4_sgpr rx = rsrc_words(p.x), rw = rsrc_words(p.w16);
@@ -600,7 +614,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
           v = floatx4{0.f, 0.f, 0.f, 0.f};
           v += acc[i][j];  // total = 0 + chunk, as the split-K reduction computes it
         }
-        epilogue<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, v);
+        if constexpr (PRE)
+          epilogue_with<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, v, eop[i][j]);
+        else
+          epilogue<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, v);
       }
     }
   }
