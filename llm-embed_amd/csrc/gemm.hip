@@ -440,6 +440,60 @@ __device__ __forceinline__ u32x4_sgpr rsrc_words(const void* p) {
   return u32x4_sgpr{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, 0xffffffffu, 0x00020000u};
 }
 
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_b64(__amdgpu_buffer_rsrc_t r, int off, uint32_t lo, uint32_t hi) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{lo, hi}, r, off, 0, 0);
+}
+__device__ __forceinline__ void st_b16(__amdgpu_buffer_rsrc_t r, int off, __half v) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, off, 0, 0);
+}
+
+// The QKV epilogue of a large-GEMM wave tile (features fb.., tokens mb..): the arithmetic of
+// epilogue_with<EPI_QKV>, with the section / head split done once per 16-feature fragment (the
+// fragment lies inside one head: D % 64 == 0), the (sequence, position) split once per token
+// fragment, and 32-bit buffer offsets instead of 64-bit pointers.
+template <int FB, int TB>
+__device__ __forceinline__ void qkv_tile(const GemmP& p, const floatx4 (&acc)[FB][TB], const floatx4 (&eop)[FB][TB],
+                                         int mb, int fb, int lane) {
+  const int lr = lane & 15, lg = lane >> 4;
+  const int D = p.D, L = p.L, Lp = p.Lp, H = p.H, M = p.M;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q), rk = make_rsrc(p.k), rv = make_rsrc(p.vt);
+  int bs[TB], ps[TB];
+#pragma unroll
+  for (int j = 0; j < TB; j++) {
+    const int m = mb + j * 16 + lr;
+    bs[j] = m / L;
+    ps[j] = m - bs[j] * L;
+  }
+#pragma unroll
+  for (int i = 0; i < FB; i++) {
+    const int f0 = fb + i * 16;  // wave-uniform
+    const int sec = f0 >= 2 * D ? 2 : (f0 >= D ? 1 : 0);
+    const int fi = f0 - sec * D + lg * 4, h = fi >> 6, e = fi & 63;
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      if (mb + j * 16 + lr >= M) continue;
+      floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+      v += acc[i][j];  // total = 0 + chunk
+      if (sec < 2) {
+        const floatx4 o = eop[i][j];
+        const float c0 = o.x, s0 = o.y, c1 = o.z, s1 = o.w;
+        const float a0 = v.x * c0 - v.y * s0, a1 = v.x * s0 + v.y * c0;
+        const float a2 = v.z * c1 - v.w * s1, a3 = v.z * s1 + v.w * c1;
+        const __half2 lo = __floats2half2_rn(a0, a1), hi = __floats2half2_rn(a2, a3);
+        const int off = (((bs[j] * H + h) * Lp + ps[j]) * 64 + e) * 2;
+        st_b64(sec == 0 ? rq : rk, off, __builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+      } else {
+        const int off = (((bs[j] * H + h) * 64 + e) * Lp + ps[j]) * 2;
+        st_b16(rv, off, __float2half_rn(v.x));
+        st_b16(rv, off + Lp * 2, __float2half_rn(v.y));
+        st_b16(rv, off + Lp * 4, __float2half_rn(v.z));
+        st_b16(rv, off + Lp * 6, __float2half_rn(v.w));
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int NS, int EPI, bool MULTI>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   constexpr int NW = WM * WN;
@@ -601,6 +655,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     }
   }
 
+  if constexpr (EPI == EPI_QKV && !MULTI) {
+    qkv_tile<FB, TB>(p, acc, eop, m0 + wm * TM, n0 + wn * TN, lane);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TB; j++) {
     const int m = m0 + wm * TM + j * 16 + lr;
