@@ -44,6 +44,7 @@ struct GemmP {
   __half* g;
   float* part;  // split-K partials [K/kchunk][M][N]
   const __half* w16;  // resident f16 copy of the weights [N][K], or null
+  LnPrologue ln;      // LayerNorm prologue of the small-M kernel
 };
 
 // GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42). The quotient
@@ -956,7 +957,10 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __r
 // global load of the block is issued before the first MFMA (one memory round trip); the chunk
 // goes through LDS in 256-wide pieces while a single MFMA chain continues across them. The
 // chunk result goes to part[chunk][m][n]; gemm_reduce adds the chunks in order.
-template <int FMT, int BM, int BN, int NPIECE, int EPI, bool DIRECT>
+// LNP > 0 (M <= 16, K = NPIECE * 256 = 768, one chunk): X = LayerNorm(ln.src + ordered sum of
+// LNP-1 partial chunks) computed in every block with ln_row's arithmetic and written as f16
+// straight into LDS for the whole K; block 0 also stores the f32 LayerNorm rows to ln.out.
+template <int FMT, int BM, int BN, int NPIECE, int EPI, bool DIRECT, int LNP = 0>
 __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
   constexpr int NT = BN * 4, TB = BM / 16, PK = 256;  // one wave per 16 features
   constexpr int LDW = PK;  // XOR-swizzled chunks (swz)
@@ -966,8 +970,10 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
   constexpr int XPT = (XCH + NT - 1) / NT;
   constexpr bool AHEAD = FMT != 0;  // f32 weights are too wide to hold every piece in registers
   constexpr int NP = AHEAD ? NPIECE : 1;
+  constexpr int KF = NPIECE * PK;  // LNP: the whole K
   __shared__ __attribute__((aligned(16))) _Float16 sW[BN][LDW];
-  __shared__ __attribute__((aligned(16))) _Float16 sX[BM][LDW];
+  __shared__ __attribute__((aligned(16))) _Float16 sX[LNP ? 1 : BM][LDW];
+  __shared__ __attribute__((aligned(16))) _Float16 sXf[LNP ? BM : 1][LNP ? KF : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n0 = blockIdx.x * BN, c = blockIdx.y, kbase = c * NPIECE * PK;
@@ -981,18 +987,60 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
       const int u = tid + i * NT;
       wr[slot][i] = load_seg<FMT>(p.w, n0 + (u >> 4), kb + (u & 15) * 16);
     }
+    if constexpr (LNP == 0) {
 #pragma unroll
-    for (int i = 0; i < XPT; i++) {
-      const int cc = tid + i * NT;
-      if (cc < XCH) {
-        const int row = cc >> 5, ch = cc & 31;
-        xr[slot][i] = row < M ? *(const uint4*)(p.x + (size_t)row * K + kb + ch * 8) : uint4{0, 0, 0, 0};
+      for (int i = 0; i < XPT; i++) {
+        const int cc = tid + i * NT;
+        if (cc < XCH) {
+          const int row = cc >> 5, ch = cc & 31;
+          xr[slot][i] = row < M ? *(const uint4*)(p.x + (size_t)row * K + kb + ch * 8) : uint4{0, 0, 0, 0};
+        }
       }
     }
   };
   if constexpr (AHEAD) {
 #pragma unroll
     for (int pc = 0; pc < NPIECE; pc++) load_piece(pc, kbase + pc * PK);
+  }
+
+  if constexpr (LNP > 0) {
+    static_assert(BM == 16 && DIRECT && KF <= 64 * MAXE, "LayerNorm prologue shape");
+    constexpr int NPART = LNP - 1, NE = KF / 64;
+    for (int r = wave; r < BM; r += NT / 64) {  // wave-uniform rows
+      float x[MAXE];
+      if (r < M) {
+        float pv[MAXE][NPART > 0 ? NPART : 1];
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+          const int j = lane + 64 * i;
+          x[i] = p.ln.src[(size_t)r * KF + j];
+#pragma unroll
+          for (int q = 0; q < NPART; q++) pv[i][q] = p.ln.part[((size_t)q * M + r) * KF + j];
+        }
+        if constexpr (NPART > 0) {  // reduce_resid_ln_kernel's order: x + (0 + p0 + p1 + ...)
+#pragma unroll
+          for (int i = 0; i < NE; i++) {
+            float t = 0.f;
+#pragma unroll
+            for (int q = 0; q < NPART; q++) t += pv[i][q];
+            x[i] = x[i] + t;
+          }
+        }
+        ln_apply(x, NE, KF, p.ln.w, p.ln.b, p.ln.eps, lane);
+        if (blockIdx.x == 0 && blockIdx.y == 0) {
+#pragma unroll
+          for (int i = 0; i < NE; i++) p.ln.out[(size_t)r * KF + lane + 64 * i] = x[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NE; i++) x[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < NE; i++) {
+        const int k = lane + 64 * i;  // chunk k/8 stored at (k/8) ^ (r & 7), as swz
+        sXf[r][(((k >> 3) ^ (r & 7)) << 3) + (k & 7)] = (_Float16)__float2half_rn(x[i]);
+      }
+    }
   }
 
   const int lr = lane & 15, lg = lane >> 4;
@@ -1011,10 +1059,12 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
     const int kb = kbase + pc * PK;
     if constexpr (!AHEAD) load_piece(0, kb);
     if (pc > 0) __syncthreads();
+    if constexpr (LNP == 0) {
 #pragma unroll
-    for (int i = 0; i < XPT; i++) {
-      const int cc = tid + i * NT;
-      if (cc < XCH) *(uint4*)&sX[cc >> 5][swz(cc >> 5, cc & 31) * 8] = xr[slot][i];
+      for (int i = 0; i < XPT; i++) {
+        const int cc = tid + i * NT;
+        if (cc < XCH) *(uint4*)&sX[cc >> 5][swz(cc >> 5, cc & 31) * 8] = xr[slot][i];
+      }
     }
 #pragma unroll
     for (int i = 0; i < WPT; i++) {
@@ -1030,7 +1080,11 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
       const half8 af = *(const half8*)&sW[wave * 16 + lr][swz(lr, ks * 4 + lg) * 8];
 #pragma unroll
       for (int j = 0; j < TB; j++) {
-        const half8 bf = *(const half8*)&sX[j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+        half8 bf;
+        if constexpr (LNP > 0)
+          bf = *(const half8*)&sXf[j * 16 + lr][(pc * (PK / 8) + swz(lr, ks * 4 + lg)) * 8];
+        else
+          bf = *(const half8*)&sX[j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
         acc[j] = mfma16(af, bf, acc[j]);
       }
     }
@@ -1094,6 +1148,34 @@ static hipError_t launch_small(const GemmP& p, hipStream_t st, bool reduce) {
   const int n = p.M * (p.N / 4);
   hipLaunchKernelGGL((gemm_reduce<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, p);
   return hipGetLastError();
+}
+
+template <int FMT, int EPI, int LNP>
+static hipError_t launch_lnx3(const GemmP& p, hipStream_t st) {
+  const dim3 grid(p.N / 64, 1), blk(256);
+  hipLaunchKernelGGL((gemm_small<FMT, 16, 64, 3, EPI, true, LNP>), grid, blk, 0, st, p);
+  return hipGetLastError();
+}
+
+template <int FMT, int EPI>
+static hipError_t launch_lnx2(const GemmP& p, hipStream_t st) {
+  switch (p.ln.part ? p.ln.nch : 0) {
+    case 0: return launch_lnx3<FMT, EPI, 1>(p, st);
+    case 4: return launch_lnx3<FMT, EPI, 5>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int EPI>
+static hipError_t launch_lnx1(int type, const GemmP& p, hipStream_t st) {
+  switch (type) {
+    case LLE_TYPE_Q8_0: return launch_lnx2<8, EPI>(p, st);
+    case LLE_TYPE_Q4_K: return launch_lnx2<12, EPI>(p, st);
+    case LLE_TYPE_Q5_K: return launch_lnx2<13, EPI>(p, st);
+    case LLE_TYPE_Q6_K: return launch_lnx2<14, EPI>(p, st);
+    case LLE_TYPE_F32: return launch_lnx2<0, EPI>(p, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int FMT, int EPI>
@@ -1193,6 +1275,27 @@ hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st) {
 // K chunks the chunk reduction, residual add and LayerNorm run as one row kernel; otherwise the
 // GEMM's residual epilogue is followed by the LayerNorm kernel. Both orders of operations are
 // identical (same reduction order, same add, same LayerNorm), so results do not depend on M.
+hipError_t launch_gemm_partials(const GemmArgs& a, hipStream_t st) {
+  const GemmP p = make_params(a);
+  if (p.M > 64 || p.K / kchunk_of(p.K) < 2) return hipErrorInvalidValue;
+  return launch_epi<EPI_RESID>(a.w->type, p, st, false);
+}
+
+bool gemm_lnx_supported(const GemmArgs& a, const LnPrologue& ln) {
+  return a.M <= 16 && a.w->K == 768 && a.w->N % 64 == 0 && (ln.part ? ln.nch == 4 : true);
+}
+
+hipError_t launch_gemm_lnx(const GemmArgs& a, int epi, const LnPrologue& ln, hipStream_t st) {
+  if (!gemm_lnx_supported(a, ln)) return hipErrorInvalidValue;
+  GemmP p = make_params(a);
+  p.ln = ln;
+  switch (epi) {
+    case EPI_QKV: return launch_lnx1<EPI_QKV>(a.w->type, p, st);
+    case EPI_GEGLU: return launch_lnx1<EPI_GEGLU>(a.w->type, p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
                                 hipStream_t st) {
   const GemmP p = make_params(a);
@@ -1220,7 +1323,7 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
   if (p.M <= 64 && (nch == 2 || nch == 3 || nch == 4 || nch == 8 || nch == 12)) {
     hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, false);
     if (e != hipSuccess) return e;
-    return launch_reduce_resid_ln(p.part, nch, p.M, p.N, p.y, h16, w, b, eps, st);
+    return launch_reduce_resid_ln(p.part, nch, p.M, p.N, p.y, p.y, h16, w, b, eps, st);
   }
   hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, true);
   if (e != hipSuccess) return e;

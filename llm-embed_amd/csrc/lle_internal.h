@@ -82,8 +82,25 @@ hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st);
 // a.y (= h) += X . W^T, then LayerNorm(h; w, b, eps) into h and h16
 hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
                                 hipStream_t st);
-hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, float* h, __half* h16, const float* w,
-                                  const float* b, float eps, hipStream_t st);
+// M <= 16, K = 768: GEMM whose X operand is LN(src [+ ordered sum of nch partials]) computed in
+// every block (ln_row's arithmetic); block 0 also writes that LayerNorm output (f32) to ln_out.
+// Replaces a LayerNorm (or reduce + residual + LayerNorm) kernel in front of the GEMM.
+struct LnPrologue {
+  const float* src;
+  const float* part;  // [nch][M][768] or null
+  int nch;
+  const float* w;
+  const float* b;
+  float eps;
+  float* out;
+};
+bool gemm_lnx_supported(const GemmArgs& a, const LnPrologue& ln);
+hipError_t launch_gemm_lnx(const GemmArgs& a, int epi, const LnPrologue& ln, hipStream_t st);
+// M <= 64, K spanning several canonical chunks: per-chunk partials only (part[c][M][N])
+hipError_t launch_gemm_partials(const GemmArgs& a, hipStream_t st);
+// h = LN(src + (0 + part[0] + ... + part[nch-1])) and h16 = f16(h); src may equal h
+hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, const float* src, float* h, __half* h16,
+                                  const float* w, const float* b, float eps, hipStream_t st);
 
 hipError_t launch_f32_to_f16(const float* x, __half* y, int64_t n, hipStream_t st);
 hipError_t launch_f16_to_f32_bits(const uint16_t* h, float* out, int64_t n, hipStream_t st);

@@ -32,8 +32,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // LayerNormInPlace (internal/ggml/ops_simd.go:7-24): one-pass sum / sum of squares in f32,
 // var = sumSq/n - mean^2, invStd = float32(1/sqrt(float64(var + eps))),
 // y = (x - mean) * invStd * w + b. One wave per row; element j = lane + 64 i.
-__device__ __forceinline__ void ln_row(float* x, int ne, int D, const float* w, const float* b, float eps,
-                                       int lane, float* hrow, __half* h16row) {
+// LayerNorm of one row held as x[i] = element lane + 64 i; x is replaced by the output y.
+__device__ __forceinline__ void ln_apply(float* x, int ne, int D, const float* w, const float* b, float eps,
+                                         int lane) {
   float wv[MAXE], bv[MAXE];  // issued before the reductions so their latency overlaps them
 #pragma unroll
   for (int i = 0; i < MAXE; i++)
@@ -56,11 +57,19 @@ __device__ __forceinline__ void ln_row(float* x, int ne, int D, const float* w, 
   const float inv = (float)(1.0 / sqrt((double)(var + eps)));
 #pragma unroll
   for (int i = 0; i < MAXE; i++)
+    if (i < ne) x[i] = (x[i] - mean) * inv * wv[i] + bv[i];
+}
+
+// LayerNormInPlace of one row into hrow (f32) and h16row (f16).
+__device__ __forceinline__ void ln_row(float* x, int ne, int D, const float* w, const float* b, float eps,
+                                       int lane, float* hrow, __half* h16row) {
+  ln_apply(x, ne, D, w, b, eps, lane);
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
     if (i < ne) {
       const int j = lane + 64 * i;
-      const float y = (x[i] - mean) * inv * wv[i] + bv[i];
-      hrow[j] = y;
-      h16row[j] = __float2half_rn(y);
+      hrow[j] = x[i];
+      h16row[j] = __float2half_rn(x[i]);
     }
 }
 

@@ -69,21 +69,22 @@ hipError_t launch_ln(float* h, __half* h16, const float* w, const float* b, floa
 // t = 0 + part[0] + part[1] + ... (gemm_reduce's order), h = h + t (the residual epilogue's add),
 // then the LayerNorm of ln_kernel with the same element-to-lane mapping and reduction tree.
 template <int NCH>
-__global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __restrict__ part, int M, int N, float* h,
-                                                              __half* h16, const float* w, const float* b,
-                                                              float eps) {
+__global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __restrict__ part, int M, int N,
+                                                              const float* src, float* h, __half* h16, const float* w,
+                                                              const float* b, float eps) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= M) return;
   const int ne = N / 64;
   float* row = h + (size_t)t * N;
+  const float* srow = src + (size_t)t * N;  // the residual (== row when updating in place)
   // every load is issued before the first add (one memory round trip); adds in chunk order
   float pv[MAXE][NCH], x[MAXE];
 #pragma unroll
   for (int i = 0; i < MAXE; i++)
     if (i < ne) {
       const int j = lane + 64 * i;
-      x[i] = row[j];
+      x[i] = srow[j];
 #pragma unroll
       for (int c = 0; c < NCH; c++) pv[i][c] = part[((size_t)c * M + t) * N + j];
     }
@@ -98,15 +99,15 @@ __global__ __launch_bounds__(256) void reduce_resid_ln_kernel(const float* __res
   ln_row(x, ne, N, w, b, eps, lane, row, h16 + (size_t)t * N);
 }
 
-hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, float* h, __half* h16, const float* w,
-                                  const float* b, float eps, hipStream_t st) {
+hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, const float* src, float* h, __half* h16,
+                                  const float* w, const float* b, float eps, hipStream_t st) {
   const dim3 g((M + 3) / 4), blk(256);
   switch (nch) {
-    case 2: hipLaunchKernelGGL(reduce_resid_ln_kernel<2>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
-    case 3: hipLaunchKernelGGL(reduce_resid_ln_kernel<3>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
-    case 4: hipLaunchKernelGGL(reduce_resid_ln_kernel<4>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
-    case 8: hipLaunchKernelGGL(reduce_resid_ln_kernel<8>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
-    case 12: hipLaunchKernelGGL(reduce_resid_ln_kernel<12>, g, blk, 0, st, part, M, N, h, h16, w, b, eps); break;
+    case 2: hipLaunchKernelGGL(reduce_resid_ln_kernel<2>, g, blk, 0, st, part, M, N, src, h, h16, w, b, eps); break;
+    case 3: hipLaunchKernelGGL(reduce_resid_ln_kernel<3>, g, blk, 0, st, part, M, N, src, h, h16, w, b, eps); break;
+    case 4: hipLaunchKernelGGL(reduce_resid_ln_kernel<4>, g, blk, 0, st, part, M, N, src, h, h16, w, b, eps); break;
+    case 8: hipLaunchKernelGGL(reduce_resid_ln_kernel<8>, g, blk, 0, st, part, M, N, src, h, h16, w, b, eps); break;
+    case 12: hipLaunchKernelGGL(reduce_resid_ln_kernel<12>, g, blk, 0, st, part, M, N, src, h, h16, w, b, eps); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -83,6 +83,7 @@ struct lle_model {
   size_t ws_T = 0, ws_heads = 0, ws_part = 0;
   int ws_B = 0;
   float* h = nullptr;
+  float* h2 = nullptr;  // second residual buffer of the fused small-batch layer schedule (16 x D)
   __half* h16 = nullptr;
   __half *q = nullptr, *k = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
   float* part = nullptr;
@@ -122,10 +123,10 @@ static void clear_graphs(lle_model* m) {
 
 static void ws_free(lle_model* m) {
   clear_graphs(m);
-  void* bufs[] = {m->h, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->kv_range, m->out};
+  void* bufs[] = {m->h, m->h2, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->kv_range, m->out};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
-  m->h = nullptr; m->h16 = nullptr; m->q = m->k = m->vt = m->attn = m->ff = nullptr;
+  m->h = nullptr; m->h2 = nullptr; m->h16 = nullptr; m->q = m->k = m->vt = m->attn = m->ff = nullptr;
   m->part = nullptr; m->ids = m->mask = m->kv_range = nullptr; m->out = nullptr;
   m->ws_T = m->ws_heads = m->ws_part = 0;
   m->ws_B = 0;
@@ -156,6 +157,7 @@ static int ensure_ws(lle_model* m, int B, int L) {
   LLE_HIP(hipStreamSynchronize(m->stream));
   ws_free(m);
   WS_ALLOC(m->h, nT * m->D * 4);
+  WS_ALLOC(m->h2, (size_t)16 * m->D * 4);
   WS_ALLOC(m->h16, nT * m->D * 2);
   WS_ALLOC(m->q, nH * 2);
   WS_ALLOC(m->k, nH * 2);
@@ -255,6 +257,76 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
   {
     Scope s(m, st, "kv_range", 0, (double)T * 4);
     LAUNCH(launch_kv_range(d_mask, B, L, m->kv_range, st));
+  }
+  // Batches of <= 16 tokens: each LayerNorm runs inside the GEMM that consumes it (every block
+  // normalises the few rows itself, block 0 keeps the f32 rows for the next residual), which
+  // removes two dependent kernels per layer. Residual stream: h (after attention) and h2 (after
+  // the FFN input LayerNorm); the down projection leaves its four chunk partials for the next
+  // layer's QKV prologue, and the last layer's go through one reduce + residual + LayerNorm.
+  if (T <= 16 && D == 768 && F == 4 * 768) {
+    for (int l = 0; l < m->n_layer; l++) {
+      Layer& ly = m->layers[l];
+      GemmArgs g{};
+      g.M = T;
+      g.rope_cos = m->rope_cos;
+      g.rope_sin = m->rope_sin;
+      g.L = L;
+      g.Lp = Lp;
+      g.n_head = H;
+      g.d_model = D;
+      g.part = m->part;
+      {
+        g.w = &ly.qkv;
+        g.x = m->h16;
+        g.q = m->q;
+        g.k = m->k;
+        g.vt = m->vt;
+        Scope s(m, st, "gemm_qkv", 2.0 * T * ly.qkv.N * ly.qkv.K, wbytes(ly.qkv) + (double)T * (D * 2 + 3 * D * 2));
+        if (l == 0) {
+          LAUNCH(launch_gemm(g, EPI_QKV, st));
+        } else {
+          const Layer& pv = m->layers[l - 1];
+          const LnPrologue ln{m->h2, m->part, 4, pv.onw, pv.onb, m->eps, m->h};
+          LAUNCH(launch_gemm_lnx(g, EPI_QKV, ln, st));
+        }
+      }
+      {
+        AttnArgs a{m->q, m->k, m->vt, d_mask, m->kv_range, m->attn, B, L, Lp, H, D};
+        Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
+        LAUNCH(launch_attention(a, st));
+      }
+      {
+        g.w = &ly.out;
+        g.x = m->attn;
+        g.y = m->h;
+        Scope s(m, st, "gemm_out_ln", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 8));
+        LAUNCH(launch_gemm(g, EPI_RESID, st));
+      }
+      {
+        g.w = &ly.upgate;
+        g.g = m->ff;
+        const LnPrologue ln{m->h, nullptr, 0, ly.anw, ly.anb, m->eps, m->h2};
+        Scope s(m, st, "gemm_upgate", 2.0 * T * ly.upgate.N * ly.upgate.K, wbytes(ly.upgate) + (double)T * (D * 4 + F * 2));
+        LAUNCH(launch_gemm_lnx(g, EPI_GEGLU, ln, st));
+      }
+      {
+        g.w = &ly.down;
+        g.x = m->ff;
+        g.y = m->h2;
+        Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 16));
+        LAUNCH(launch_gemm_partials(g, st));
+      }
+    }
+    {
+      const Layer& last = m->layers[m->n_layer - 1];
+      Scope s(m, st, "ln", 0, (double)T * D * 26);
+      LAUNCH(launch_reduce_resid_ln(m->part, 4, T, D, m->h2, m->h, m->h16, last.onw, last.onb, m->eps, st));
+    }
+    if (d_out) {
+      Scope s(m, st, "pool", 0, (double)T * D * 4);
+      LAUNCH(launch_pool(m->h, d_mask, B, L, D, out_dim, d_out, st));
+    }
+    return LLE_OK;
   }
   for (int l = 0; l < m->n_layer; l++) {
     Layer& ly = m->layers[l];
