@@ -26,46 +26,9 @@ namespace lle {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int AQ = 64;   // queries per block
 constexpr int AK = 64;   // keys per tile
 constexpr int HD = 64;   // head dim
 constexpr int APAD = 8;
-
-__global__ void kv_range_kernel(const int32_t* __restrict__ mask, int L, int32_t* __restrict__ range) {
-  const int b = blockIdx.x;
-  int lo = L, hi = -1;
-  for (int i = threadIdx.x; i < L; i += blockDim.x) {
-    if (mask[(size_t)b * L + i] != 0) {
-      lo = min(lo, i);
-      hi = max(hi, i);
-    }
-  }
-  __shared__ int slo[256], shi[256];
-  slo[threadIdx.x] = lo;
-  shi[threadIdx.x] = hi;
-  __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      slo[threadIdx.x] = min(slo[threadIdx.x], slo[threadIdx.x + s]);
-      shi[threadIdx.x] = max(shi[threadIdx.x], shi[threadIdx.x + s]);
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    if (shi[0] < 0) {  // no valid key: uniform softmax over all L keys
-      range[2 * b] = 0;
-      range[2 * b + 1] = L;
-    } else {
-      range[2 * b] = slo[0];
-      range[2 * b + 1] = shi[0] + 1;
-    }
-  }
-}
-
-hipError_t launch_kv_range(const int32_t* mask, int B, int L, int32_t* kv_range, hipStream_t st) {
-  hipLaunchKernelGGL(kv_range_kernel, dim3(B), dim3(256), 0, st, mask, L, kv_range);
-  return hipGetLastError();
-}
 
 __device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const floatx4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -103,7 +66,40 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
       qf[ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
-  const int klo = a.kv_range[2 * b], khi = a.kv_range[2 * b + 1];
+  // [klo, khi): from the first to one past the last valid key of the sequence (all L keys when
+  // none is valid: the softmax is then uniform over every key)
+  __shared__ int sLo[NW], sHi[NW];
+  int klo, khi;
+  {
+    const int32_t* mrow = a.mask + (size_t)b * L;
+    int lo = L, hi = -1;
+#pragma unroll 4
+    for (int i = tid; i < L; i += NT) {
+      if (mrow[i] != 0) {
+        lo = min(lo, i);
+        hi = max(hi, i);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      lo = min(lo, __shfl_xor(lo, o));
+      hi = max(hi, __shfl_xor(hi, o));
+    }
+    if (lane == 0) {
+      sLo[wave] = lo;
+      sHi[wave] = hi;
+    }
+    __syncthreads();
+    lo = sLo[0];
+    hi = sHi[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) {
+      lo = min(lo, sLo[w]);
+      hi = max(hi, sHi[w]);
+    }
+    klo = hi < 0 ? 0 : lo;
+    khi = hi < 0 ? L : hi + 1;
+  }
   const int t0 = klo / AK, t1 = (khi + AK - 1) / AK;
   if (qt * AQB >= khi) {
     // every query of this block lies past the last valid key, so it is padding (mask 0):

@@ -1004,41 +1004,53 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
   }
 
   if constexpr (LNP > 0) {
-    static_assert(BM == 16 && DIRECT && KF <= 64 * MAXE, "LayerNorm prologue shape");
+    static_assert(BM == 16 && DIRECT && KF <= 64 * MAXE && NT == 256, "LayerNorm prologue shape");
     constexpr int NPART = LNP - 1, NE = KF / 64;
-    for (int r = wave; r < BM; r += NT / 64) {  // wave-uniform rows
-      float x[MAXE];
-      if (r < M) {
-        float pv[MAXE][NPART > 0 ? NPART : 1];
+    // wave w normalises rows w, w + 4 (and w + 8, w + 12): each pair's loads are issued together
 #pragma unroll
-        for (int i = 0; i < NE; i++) {
-          const int j = lane + 64 * i;
-          x[i] = p.ln.src[(size_t)r * KF + j];
+    for (int r0 = 0; r0 < BM; r0 += 8) {
+      float x[2][MAXE];
+      float pv[2][MAXE][NPART > 0 ? NPART : 1];
 #pragma unroll
-          for (int q = 0; q < NPART; q++) pv[i][q] = p.ln.part[((size_t)q * M + r) * KF + j];
-        }
-        if constexpr (NPART > 0) {  // reduce_resid_ln_kernel's order: x + (0 + p0 + p1 + ...)
+      for (int h = 0; h < 2; h++) {
+        const int r = r0 + wave + 4 * h;
+        if (r < M) {
 #pragma unroll
           for (int i = 0; i < NE; i++) {
-            float t = 0.f;
+            const int j = lane + 64 * i;
+            x[h][i] = p.ln.src[(size_t)r * KF + j];
 #pragma unroll
-            for (int q = 0; q < NPART; q++) t += pv[i][q];
-            x[i] = x[i] + t;
+            for (int q = 0; q < NPART; q++) pv[h][i][q] = p.ln.part[((size_t)q * M + r) * KF + j];
           }
         }
-        ln_apply(x, NE, KF, p.ln.w, p.ln.b, p.ln.eps, lane);
-        if (blockIdx.x == 0 && blockIdx.y == 0) {
-#pragma unroll
-          for (int i = 0; i < NE; i++) p.ln.out[(size_t)r * KF + lane + 64 * i] = x[i];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < NE; i++) x[i] = 0.f;
       }
 #pragma unroll
-      for (int i = 0; i < NE; i++) {
-        const int k = lane + 64 * i;  // chunk k/8 stored at (k/8) ^ (r & 7), as swz
-        sXf[r][(((k >> 3) ^ (r & 7)) << 3) + (k & 7)] = (_Float16)__float2half_rn(x[i]);
+      for (int h = 0; h < 2; h++) {
+        const int r = r0 + wave + 4 * h;
+        if (r < M) {
+          if constexpr (NPART > 0) {  // reduce_resid_ln_kernel's order: x + (0 + p0 + p1 + ...)
+#pragma unroll
+            for (int i = 0; i < NE; i++) {
+              float t = 0.f;
+#pragma unroll
+              for (int q = 0; q < NPART; q++) t += pv[h][i][q];
+              x[h][i] = x[h][i] + t;
+            }
+          }
+          ln_apply(x[h], NE, KF, p.ln.w, p.ln.b, p.ln.eps, lane);
+          if (blockIdx.x == 0 && blockIdx.y == 0) {
+#pragma unroll
+            for (int i = 0; i < NE; i++) p.ln.out[(size_t)r * KF + lane + 64 * i] = x[h][i];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < NE; i++) x[h][i] = 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+          const int k = lane + 64 * i;  // chunk k/8 stored at (k/8) ^ (r & 7), as swz
+          sXf[r][(((k >> 3) ^ (r & 7)) << 3) + (k & 7)] = (_Float16)__float2half_rn(x[h][i]);
+        }
       }
     }
   }

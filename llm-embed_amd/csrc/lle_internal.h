@@ -133,11 +133,9 @@ struct AttnArgs {
   const __half* k;
   const __half* vt;
   const int32_t* mask;   // [B][L]
-  const int32_t* kv_range;  // [B][2] key tile range [lo, hi) in keys
   __half* out;           // [B*L][D]
   int B, L, Lp, H, D;
 };
-hipError_t launch_kv_range(const int32_t* mask, int B, int L, int32_t* kv_range, hipStream_t st);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 
 hipError_t launch_pool(const float* h, const int32_t* mask, int B, int L, int D, int out_dim, float* out,

@@ -87,7 +87,7 @@ struct lle_model {
   __half* h16 = nullptr;
   __half *q = nullptr, *k = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
   float* part = nullptr;
-  int32_t *ids = nullptr, *mask = nullptr, *kv_range = nullptr, *status = nullptr;
+  int32_t *ids = nullptr, *mask = nullptr, *status = nullptr;
   float* out = nullptr;
   // HIP graphs of small forwards, keyed by shape, pointers and stream
   struct GraphEntry {
@@ -123,11 +123,11 @@ static void clear_graphs(lle_model* m) {
 
 static void ws_free(lle_model* m) {
   clear_graphs(m);
-  void* bufs[] = {m->h, m->h2, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->kv_range, m->out};
+  void* bufs[] = {m->h, m->h2, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->out};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   m->h = nullptr; m->h2 = nullptr; m->h16 = nullptr; m->q = m->k = m->vt = m->attn = m->ff = nullptr;
-  m->part = nullptr; m->ids = m->mask = m->kv_range = nullptr; m->out = nullptr;
+  m->part = nullptr; m->ids = m->mask = nullptr; m->out = nullptr;
   m->ws_T = m->ws_heads = m->ws_part = 0;
   m->ws_B = 0;
 }
@@ -167,7 +167,6 @@ static int ensure_ws(lle_model* m, int B, int L) {
   if (nP) WS_ALLOC(m->part, nP * 4);
   WS_ALLOC(m->ids, nT * 4);
   WS_ALLOC(m->mask, nT * 4);
-  WS_ALLOC(m->kv_range, (size_t)nB * 8);
   WS_ALLOC(m->out, (size_t)nB * m->D * 4);
   m->ws_T = nT;
   m->ws_heads = nH;
@@ -254,10 +253,6 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
     Scope s(m, st, "embed_ln", 0, (double)T * (m->tok_row_bytes + D * 6));
     LAUNCH(launch_embed_ln(a, st));
   }
-  {
-    Scope s(m, st, "kv_range", 0, (double)T * 4);
-    LAUNCH(launch_kv_range(d_mask, B, L, m->kv_range, st));
-  }
   // Batches of <= 16 tokens: each LayerNorm runs inside the GEMM that consumes it (every block
   // normalises the few rows itself, block 0 keeps the f32 rows for the next residual), which
   // removes two dependent kernels per layer. Residual stream: h (after attention) and h2 (after
@@ -291,7 +286,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
         }
       }
       {
-        AttnArgs a{m->q, m->k, m->vt, d_mask, m->kv_range, m->attn, B, L, Lp, H, D};
+        AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D};
         Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
         LAUNCH(launch_attention(a, st));
       }
@@ -349,7 +344,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
       LAUNCH(launch_gemm(g, EPI_QKV, st));
     }
     {
-      AttnArgs a{m->q, m->k, m->vt, d_mask, m->kv_range, m->attn, B, L, Lp, H, D};
+      AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D};
       Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
       LAUNCH(launch_attention(a, st));
     }
