@@ -245,6 +245,41 @@ def main():
         extras["config3_Q4_K_M"] = run_cfg(3, "Q4_K_M", 10)
         extras["config5_Q8_0"] = run_cfg(5, "Q8_0", 5)
 
+        # Text path (EmbedBatch over strings): native host tokeniser, then lle_embed_texts'
+        # length-ordered batches, against the same texts in input order, 256 per padded batch.
+        corpus = synth.texts(4096, seed=0x7E57, min_words=4, max_words=110)
+        nbytes = sum(len(t.encode()) for t in corpus)
+        tk = emb.tokenizer
+        tk.encode_batch(corpus[:256], model.max_seq_len, prefix=emb.task_prefix)
+        a = time.perf_counter()
+        _, _, cnt = tk.encode_batch(corpus, model.max_seq_len, prefix=emb.task_prefix)
+        tok_s = time.perf_counter() - a
+        emb.embed_texts(corpus[:512])
+        a = time.perf_counter()
+        vec = emb.embed_texts(corpus)
+        e2e_s = time.perf_counter() - a
+        a = time.perf_counter()
+        padded_tokens = 0
+        naive = []
+        for i in range(0, len(corpus), 256):
+            ib, mb, _ = tk.encode_batch(corpus[i:i + 256], model.max_seq_len, prefix=emb.task_prefix)
+            padded_tokens += ib.size
+            naive.append(emb.embed_padded(ib, mb))
+        naive_s = time.perf_counter() - a
+        naive = np.concatenate(naive)
+        assert np.array_equal(naive.view(np.uint32), vec.view(np.uint32)), "text path: batching changed a row"
+        extras["texts"] = dict(
+            texts=len(corpus), bytes=nbytes, tokens=int(cnt.sum()), mean_tokens=float(cnt.mean()),
+            tokenize_ms=1e3 * tok_s, tokenize_mb_per_s=nbytes / tok_s / 1e6, tokenize_tokens_per_s=cnt.sum() / tok_s,
+            e2e_texts_per_s=len(corpus) / e2e_s, e2e_valid_tokens_per_s=cnt.sum() / e2e_s,
+            input_order_texts_per_s=len(corpus) / naive_s,
+            input_order_padding_fraction=1 - cnt.sum() / padded_tokens,
+            note="synthetic texts (synth.texts) over the synthetic 30522-token vocabulary, config-4 model; e2e = "
+                 "tokenise + ordered batches + GPU + copies; input order = 256-text padded batches, same rows bit for bit")
+        log(f"[bench] texts: tokenise {nbytes / tok_s / 1e6:.1f} MB/s ({cnt.sum() / tok_s / 1e6:.2f} M tok/s); "
+            f"embed_texts {len(corpus) / e2e_s:.0f} texts/s vs {len(corpus) / naive_s:.0f} in input order "
+            f"({100 * extras['texts']['input_order_padding_fraction']:.0f}% padding)")
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if args.cpu_seqs > 0:

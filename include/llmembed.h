@@ -161,6 +161,42 @@ int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y);
  * then Y f32 [M][N]; enqueued on stream. */
 int32_t lle_gemm_async(const lle_weight* w, const float* d_X, void* d_x16, int32_t M, float* d_Y, void* stream);
 
+/* ---- Host tokeniser (no GPU use) ----------------------------------------------------------
+ * WordPieceTokenizer (internal/embed/tokenizer.go:15-19): nomic's "▁"-prefixed vocabulary,
+ * greedy longest match over the bytes of each lowercased, whitespace/punctuation-split word. */
+typedef struct lle_tokenizer lle_tokenizer;
+
+/* LoadTokenizer (tokenizer.go:22-45): the vocabulary is the GGUF metadata string array
+ * `tokenizer.ggml.tokens`, read as readGGUFStringArray does (:198-306). */
+int32_t lle_tokenizer_load_gguf(const char* path, lle_tokenizer** out);
+/* The same from a token list: tokens[i] of lens[i] bytes has id i (a later duplicate wins). */
+int32_t lle_tokenizer_create(const char* const* tokens, const int64_t* lens, int32_t n, lle_tokenizer** out);
+int32_t lle_tokenizer_destroy(lle_tokenizer* t);
+/* VocabSize (tokenizer.go:145-148). */
+int32_t lle_tokenizer_vocab_size(const lle_tokenizer* t, int32_t* n);
+/* Encode (tokenizer.go:47-78) of text[0..len) (len < 0: NUL-terminated): [CLS]=101, pieces,
+ * [SEP]=102, cut to max_len (>= 1) with [SEP] last; the mask is all ones. Writes the first
+ * min(count, cap) ids; *n_out = count. */
+int32_t lle_tokenize(const lle_tokenizer* t, const char* text, int64_t len, int32_t max_len, int32_t* ids,
+                     int32_t cap, int32_t* n_out);
+/* Encode(prefix + texts[i]) for n texts on host threads (lens NULL: NUL-terminated texts;
+ * prefix_len < 0: NUL-terminated prefix). n_tok[i] = token count. With ids != NULL, also
+ * writes the right-padded batch ids / mask [n][L] (pad id 0, mask 0); LLE_EINVAL when a text
+ * needs more than L tokens (call with ids NULL first to size L). */
+int32_t lle_tokenize_batch(const lle_tokenizer* t, const char* const* texts, const int64_t* lens, int32_t n,
+                           const char* prefix, int64_t prefix_len, int32_t max_len, int32_t L, int32_t* ids,
+                           int32_t* mask, int32_t* n_tok);
+
+/* EmbedBatch over text (internal/embed/embedder.go:46-133): out row i = Embed(prefix + texts[i])
+ * with max_len = the model's context_length, bit for bit the row lle_embed gives for that
+ * text's ids. Texts are tokenised on host threads, ordered by token count and run in batches
+ * of at most max_batch_tokens padded tokens (<= 0: 32768), each padded only to its longest
+ * text; past 4096 padded tokens a batch also ends before a text shorter than half its
+ * longest. out: n x min(out_dim, d_model), in input order. Synchronous. */
+int32_t lle_embed_texts(lle_model* m, const lle_tokenizer* t, const char* const* texts, const int64_t* lens,
+                        int32_t n, const char* prefix, int64_t prefix_len, int32_t out_dim,
+                        int32_t max_batch_tokens, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "lle_internal.h"
+#include "tokenizer.h"
 
 namespace lle {
 
@@ -810,6 +811,53 @@ int32_t lle_embed_batch(lle_model* m, const int32_t* ids, const int32_t* mask, i
                         float* out) {
   if (out_dim < 1) out_dim = 1;
   return run_host(m, ids, mask, B, L, out_dim, out, nullptr);
+}
+
+int32_t lle_embed_texts(lle_model* m, const lle_tokenizer* t, const char* const* texts, const int64_t* lens,
+                        int32_t n, const char* prefix, int64_t prefix_len, int32_t out_dim, int32_t max_batch_tokens,
+                        float* out) {
+  if (!m || !t || n < 0 || (n > 0 && (!texts || !out)) || (prefix_len > 0 && !prefix))
+    return fail(LLE_EINVAL, "bad argument");
+  if (n == 0) return LLE_OK;
+  if (out_dim < 1) out_dim = 1;
+  if (prefix && prefix_len < 0) prefix_len = (int64_t)strlen(prefix);
+  // the GEMMs address [tokens][d_ff] f16 with 32-bit offsets (check_batch)
+  const int64_t tok_cap = INT32_MAX / (2 * (int64_t)std::max(m->F, m->D));
+  const int64_t budget = max_batch_tokens > 0 ? std::min<int64_t>(max_batch_tokens, tok_cap) : std::min<int64_t>(32768, tok_cap);
+  std::vector<std::vector<int32_t>> v;
+  lle::tokenize_many(t->tok, texts, lens, n, prefix, prefix_len, m->max_seq, &v);
+  // longest first; equal lengths keep input order
+  std::vector<int32_t> order((size_t)n);
+  for (int32_t i = 0; i < n; i++) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return v[a].size() > v[b].size(); });
+  const int od = std::min(out_dim, m->D);
+  std::vector<int32_t> ids, mask;
+  std::vector<float> res;
+  for (int32_t i = 0; i < n;) {
+    const int L = (int)v[order[i]].size();
+    const int64_t cap = std::max<int64_t>(budget, L);
+    // a batch ends at the token budget, or, once it holds 4096 padded tokens (a forward's
+    // fixed cost is worth ~1-2k tokens), at the first text shorter than half its longest
+    int32_t j = i + 1;
+    while (j < n && (int64_t)(j - i + 1) * L <= cap &&
+           !((int64_t)(j - i) * L >= 4096 && 2 * (int64_t)v[order[j]].size() < L))
+      j++;
+    const int B = j - i;
+    ids.assign((size_t)B * L, 0);
+    mask.assign((size_t)B * L, 0);
+    for (int k = 0; k < B; k++) {
+      const std::vector<int32_t>& s = v[order[i + k]];
+      std::copy(s.begin(), s.end(), ids.begin() + (size_t)k * L);
+      std::fill(mask.begin() + (size_t)k * L, mask.begin() + (size_t)k * L + s.size(), 1);
+    }
+    res.resize((size_t)B * od);
+    const int rc = run_host(m, ids.data(), mask.data(), B, L, out_dim, res.data(), nullptr);
+    if (rc) return rc;
+    for (int k = 0; k < B; k++)
+      memcpy(out + (size_t)order[i + k] * od, res.data() + (size_t)k * od, sizeof(float) * od);
+    i = j;
+  }
+  return LLE_OK;
 }
 
 int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L, float* hidden) {

@@ -6,6 +6,7 @@ mirror of the reference's embed API plus the GGUF tooling used by tests and benc
 from . import gguf, quant, synth  # noqa: F401
 from ._lib import LLEError, Weight, dequant, f16_to_f32, info, init, lib  # noqa: F401
 from .embedder import BertModel, Embedder  # noqa: F401
+from .tokenizer import WordPieceTokenizer  # noqa: F401
 
 __all__ = ["gguf", "quant", "synth", "LLEError", "Weight", "dequant", "f16_to_f32", "info", "init", "lib",
-           "BertModel", "Embedder"]
+           "BertModel", "Embedder", "WordPieceTokenizer"]

@@ -6,9 +6,11 @@ Reference: internal/embed/embedder.go
   (*Embedder).Embed(text)                                :46-71
   (*Embedder).EmbedBatch(texts)                          :75-133
   Dim / SetTargetDim / Model                             :136-153
-Tokenisation (internal/embed/tokenizer.go) is host string work outside this path, so Embed and
-EmbedBatch take token ids (what Encode returns: [CLS] ... [SEP], mask all ones). EmbedBatch is
-truly batched: one padded [B][L] forward on the GPU, each row bit-identical to Embed of that row.
+Embed and EmbedBatch take text, as the reference's do: TaskPrefix + text is tokenised by the
+library's native tokeniser (internal/embed/tokenizer.go restated in C++) and embedded on the GPU.
+They also take token ids (what Encode returns: [CLS] ... [SEP], mask all ones). EmbedBatch is
+truly batched: texts are ordered by length and run as padded [B][L] forwards, each row
+bit-identical to Embed of that text.
 """
 from __future__ import annotations
 
@@ -18,6 +20,7 @@ import numpy as np
 
 from . import _lib
 from ._lib import LLEError, check, ptr
+from .tokenizer import WordPieceTokenizer, _as_bytes, _TextArray
 
 
 class BertModel:
@@ -76,21 +79,31 @@ class BertModel:
 class Embedder:
     """Public embedding API (embedder.go:11-16)."""
 
-    def __init__(self, model: BertModel):
+    def __init__(self, model: BertModel, tokenizer: WordPieceTokenizer | None = None):
         self._model = model
+        self.tokenizer = tokenizer
         self.target_dim = model.hidden_dim
-        self.task_prefix = "search_query: "  # embedder.go:40; applies to text, kept for API parity
+        self.task_prefix = "search_query: "  # embedder.go:40, prepended to text (:48)
 
     @classmethod
     def load(cls, model_path: str) -> "Embedder":
+        """Load (embedder.go:19-42): model (uploaded, weights resident) and tokenizer."""
         try:
             m = BertModel.load(model_path)
         except LLEError as e:
             raise LLEError(e.code, f"embed: load model: {e}") from None
-        return cls(m)
+        return cls(m, WordPieceTokenizer.load(model_path))
+
+    def _tok(self) -> WordPieceTokenizer:
+        if self.tokenizer is None:
+            raise LLEError(-1, "embed: no tokenizer (construct with one, or use Embedder.load)")
+        return self.tokenizer
 
     def embed(self, ids, mask=None) -> np.ndarray:
-        """Embed (embedder.go:46-71): forward + MeanPool + L2Normalize (+ Matryoshka)."""
+        """Embed (embedder.go:46-71): forward + MeanPool + L2Normalize (+ Matryoshka). `ids` is
+        text (str / bytes: TaskPrefix + text is tokenised) or one sequence of token ids."""
+        if isinstance(ids, (str, bytes, bytearray)):
+            return self.embed_batch([ids])[0]
         ids = np.ascontiguousarray(ids, np.int32).reshape(-1)
         mask = np.ones_like(ids) if mask is None else np.ascontiguousarray(mask, np.int32).reshape(-1)
         out = np.empty(min(self.target_dim, self._model.hidden_dim), np.float32)
@@ -99,12 +112,26 @@ class Embedder:
             raise LLEError(rc, f"embed: forward: {_lib.lib().lle_last_error().decode()}")
         return out
 
+    def embed_texts(self, texts, max_batch_tokens: int = 0) -> np.ndarray:
+        """EmbedBatch over text through lle_embed_texts: [n][dim], row i = Embed(texts[i])."""
+        arr = _TextArray(texts)
+        pb = _as_bytes(self.task_prefix)
+        out = np.empty((arr.n, min(self.target_dim, self._model.hidden_dim)), np.float32)
+        if arr.n:
+            rc = _lib.lib().lle_embed_texts(self._model.h, self._tok().h, C.cast(arr.ptrs, C.c_void_p), ptr(arr.lens),
+                                            arr.n, pb, len(pb), self.target_dim, max_batch_tokens, ptr(out))
+            if rc:
+                raise LLEError(rc, f"embed: batch: {_lib.lib().lle_last_error().decode()}")
+        return out
+
     def embed_batch(self, seqs) -> list | None:
-        """EmbedBatch (embedder.go:75-133) as one padded batched forward. `seqs` is a list of
-        token-id sequences; returns a list of vectors in input order."""
+        """EmbedBatch (embedder.go:75-133), truly batched. `seqs` is a list of texts (str /
+        bytes) or of token-id sequences; returns a list of vectors in input order."""
         n = len(seqs)
         if n == 0:
             return None
+        if all(isinstance(s, (str, bytes, bytearray)) for s in seqs):
+            return list(self.embed_texts(seqs))
         if n == 1:
             return [self.embed(seqs[0])]
         lens = [len(s) for s in seqs]

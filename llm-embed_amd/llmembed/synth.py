@@ -54,15 +54,112 @@ def mixture_types(mix: str, layer: int) -> dict:
     raise ValueError(f"unknown mixture {mix}")
 
 
+# --------------------------------------------------------------------------------------
+# Synthetic vocabulary and text. The real nomic vocabulary (BERT uncased WordPiece as llama.cpp
+# converts it: word-initial pieces carry "▁", continuation pieces lose their "##") is not
+# available, so the vocabulary is generated in that shape: specials at BERT's ids, single
+# characters with and without "▁", then words of a pseudo-English syllable lexicon (with "▁")
+# and continuation pieces (without).
+
+VOCAB_SEED = 0x70C4B
+_SYL_ONSETS = ["", "b", "c", "d", "f", "g", "h", "j", "k", "l", "m", "n", "p", "r", "s", "t", "v", "w", "z",
+               "br", "ch", "cl", "cr", "dr", "fl", "gr", "pl", "pr", "sh", "st", "th", "tr"]
+_SYL_VOWELS = ["a", "e", "i", "o", "u", "ai", "ea", "ee", "io", "ou", "y"]
+_SYL_CODAS = ["", "", "", "n", "r", "s", "t", "l", "m", "nd", "ng", "st", "ck"]
+_EXTRA_CHARS = ("àáâäçèéêëìíîïñòóôöùúûüýÿßøåæœ"  # Latin-1 / Latin Extended lowercase
+                "αβγδεζηθικλμνξοπρστυφχψω"        # Greek
+                "абвгдежзийклмнопрстуфхцчшщыьэюя"  # Cyrillic
+                "的一是不了在人有我他这个们中来上大为和国地到以说时要就出会")  # CJK
+
+
+def lexicon(n: int, seed: int = VOCAB_SEED) -> list:
+    """n distinct pseudo-English words of 1-4 syllables (deterministic)."""
+    rng = np.random.default_rng(seed)
+    words, seen = [], set()
+    while len(words) < n:
+        k = int(rng.choice([1, 2, 2, 3, 3, 4]))
+        w = "".join(_SYL_ONSETS[rng.integers(len(_SYL_ONSETS))] + _SYL_VOWELS[rng.integers(len(_SYL_VOWELS))] +
+                    _SYL_CODAS[rng.integers(len(_SYL_CODAS))] for _ in range(k))
+        if 2 <= len(w) <= 16 and w not in seen:
+            seen.add(w)
+            words.append(w)
+    return words
+
+
 def _tokens(vocab: int) -> list:
-    toks = [f"[unused{i}]" for i in range(vocab)]
+    """Vocabulary of `vocab` distinct tokens: [PAD]=0, [UNK]=100, [CLS]=101, [SEP]=102,
+    [MASK]=103, [unusedN] fillers below 999, then characters, words and pieces."""
+    toks = [f"[unused{i}]" for i in range(min(vocab, 999))]
     toks[0] = "[PAD]"
     for i, s in {100: "[UNK]", 101: "[CLS]", 102: "[SEP]", 103: "[MASK]"}.items():
         if i < vocab:
             toks[i] = s
-    for i in range(1000, vocab):
-        toks[i] = f"▁t{i}"
-    return toks
+    seen = set(toks)
+    extra = []
+
+    def add(t):
+        if t not in seen:
+            seen.add(t)
+            extra.append(t)
+
+    chars = [chr(c) for c in range(0x21, 0x7F) if not "A" <= chr(c) <= "Z"] + list(_EXTRA_CHARS)
+    for c in chars:
+        add("▁" + c)
+        add(c)
+    for w in ("hello", "world", "search", "query", "document", "what", "is", "machine", "learning"):
+        add("▁" + w)
+    for suf in ("s", "es", "ed", "ing", "er", "ers", "ly", "tion", "ment", "ness", "able", "al", "ic", "ize"):
+        add(suf)
+    room = max(0, vocab - len(toks) - len(extra))
+    words = lexicon(room)
+    n_words = (room * 3) // 4
+    for w in words[:n_words]:
+        add("▁" + w)
+    # continuation pieces: syllables and word tails
+    for on in _SYL_ONSETS:
+        for v in _SYL_VOWELS:
+            for cd in _SYL_CODAS:
+                if len(toks) + len(extra) < vocab:
+                    add(on + v + cd)
+    for w in words[n_words:]:
+        if len(toks) + len(extra) >= vocab:
+            break
+        add(w[len(w) // 2:])
+    i = 0
+    while len(toks) + len(extra) < vocab:  # top up with digit strings
+        add(str(i))
+        i += 1
+    return (toks + extra)[:vocab]
+
+
+def texts(n: int, seed: int, min_words: int = 4, max_words: int = 90) -> list:
+    """n synthetic texts: sentences over the lexicon (mostly in-vocabulary words, some unseen
+    words that split into pieces), numbers, punctuation, capitals, a little non-ASCII."""
+    rng = np.random.default_rng(seed)
+    lex = lexicon(6000)
+    out = []
+    for _ in range(n):
+        k = int(rng.integers(min_words, max_words + 1))
+        ws = []
+        for j in range(k):
+            r = rng.random()
+            if r < 0.75:
+                w = lex[min(int(rng.zipf(1.3)) - 1, len(lex) - 1)]
+            elif r < 0.88:
+                w = lex[int(rng.integers(len(lex)))] + lex[int(rng.integers(len(lex)))][:3]
+            elif r < 0.93:
+                w = str(int(rng.integers(0, 100000)))
+            elif r < 0.97:
+                w = "".join(_EXTRA_CHARS[int(rng.integers(len(_EXTRA_CHARS)))] for _ in range(int(rng.integers(1, 4))))
+            else:
+                w = "🙂" if rng.random() < 0.5 else "naïve"
+            if j == 0 or rng.random() < 0.08:
+                w = w[:1].upper() + w[1:]
+            if rng.random() < 0.1:
+                w += ",.;:!?"[int(rng.integers(6))]
+            ws.append(w)
+        out.append(" ".join(ws))
+    return out
 
 
 def build_tensors(spec: ModelSpec, mix: str, seed: int, qkv_std: float = 0.02):
@@ -135,7 +232,7 @@ def cache_dir() -> str:
 def model_path(spec: ModelSpec, mix: str, seed: int, qkv_std: float = 0.02) -> str:
     """Write (once) and return the path of a synthetic GGUF for (spec, mix, seed)."""
     name = (f"nomicbert_L{spec.n_layer}_d{spec.d_model}_h{spec.n_head}_f{spec.d_ff}_v{spec.vocab}"
-            f"_c{spec.ctx}_{mix}_s{seed}" + ("" if qkv_std == 0.02 else f"_q{qkv_std:g}") + ".gguf")
+            f"_c{spec.ctx}_{mix}_s{seed}" + ("" if qkv_std == 0.02 else f"_q{qkv_std:g}") + "_tk2.gguf")
     path = os.path.join(cache_dir(), name)
     if not os.path.exists(path):
         kvs, tensors = build_tensors(spec, mix, seed, qkv_std)
