@@ -225,16 +225,26 @@ def main():
             mm.set_timing(False)
             o_c = do.download((Bc, D), np.float32)
             assert np.all(np.isfinite(o_c)), f"config {cfg} {mix}: non-finite output"
+            # host-pointer entry point: padding is packed away before the first kernel
+            emb_c = llmembed.Embedder(mm)
+            h_c = emb_c.embed_padded(ids_c, mask_c)
+            assert np.array_equal(h_c.view(np.uint32), o_c.view(np.uint32)), f"config {cfg}: packed != padded"
+            t_c = time.perf_counter()
+            for _ in range(steps):
+                emb_c.embed_padded(ids_c, mask_c)
+            host_s = (time.perf_counter() - t_c) / steps
             tot_ms = sum(v["total_ms"] for v in kt_c.values())
             ms = 1000.0 * (t_b - t_a) / steps
             r = dict(mix=mix, batch=int(Bc), seq_len=int(Lc), valid_tokens=int(mask_c.sum()),
                      emb_per_s=Bc * steps / (t_b - t_a), ms_per_step=ms,
+                     host_api_packed_emb_per_s=Bc / host_s, host_api_packed_ms=1e3 * host_s,
                      shares={k: round(v["total_ms"] / tot_ms, 4) for k, v in kt_c.items()})
             if "attention" in kt_c:
                 at = kt_c["attention"]
                 r["attention_share"] = at["total_ms"] / tot_ms
                 r["attention_algorithmic_gbs"] = at["bytes"] / (at["total_ms"] * 1e-3) / 1e9
-            log(f"[bench] config {cfg} {mix}: {r['emb_per_s']:.1f} emb/s, {ms:.3f} ms/step"
+            log(f"[bench] config {cfg} {mix}: {r['emb_per_s']:.1f} emb/s, {ms:.3f} ms/step; host API (packed rows) "
+                f"{Bc / host_s:.1f} emb/s"
                 + (f", attention {100 * r['attention_share']:.1f}% of kernel time at {r['attention_algorithmic_gbs']:.0f} GB/s (Q,K,V,O bytes)"
                    if "attention_share" in r else ""))
             mm.close()

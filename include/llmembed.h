@@ -124,7 +124,8 @@ int32_t lle_embed(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t
 /* Batched embed: B right-padded rows of length L (mask 1 = token, 0 = padding). Each row's
  * result equals lle_embed on that row bit for bit (batch invariance, as the reference's
  * EmbedBatch == Embed tests require: internal/embed/embedder_test.go:139-144,246-251).
- * out: B x min(out_dim, d_model). */
+ * Positions after a row's last mask-1 token are not computed (packed rows): they cannot reach
+ * the embedding. out: B x min(out_dim, d_model). */
 int32_t lle_embed_batch(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L,
                         int32_t out_dim, float* out);
 
@@ -189,10 +190,10 @@ int32_t lle_tokenize_batch(const lle_tokenizer* t, const char* const* texts, con
 
 /* EmbedBatch over text (internal/embed/embedder.go:46-133): out row i = Embed(prefix + texts[i])
  * with max_len = the model's context_length, bit for bit the row lle_embed gives for that
- * text's ids. Texts are tokenised on host threads, ordered by token count and run in batches
- * of at most max_batch_tokens padded tokens (<= 0: 32768), each padded only to its longest
- * text; past 4096 padded tokens a batch also ends before a text shorter than half its
- * longest. out: n x min(out_dim, d_model), in input order. Synchronous. */
+ * text's ids. Texts are tokenised on host threads, ordered by token count (longest first) and
+ * run in batches of at most max_batch_tokens tokens (<= 0: 32768); padding is not computed
+ * (packed rows, as lle_embed_batch). out: n x min(out_dim, d_model), in input order.
+ * Synchronous. */
 int32_t lle_embed_texts(lle_model* m, const lle_tokenizer* t, const char* const* texts, const int64_t* lens,
                         int32_t n, const char* prefix, int64_t prefix_len, int32_t out_dim,
                         int32_t max_batch_tokens, float* out);

@@ -52,6 +52,10 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
   const int L = a.L, Lp = a.Lp, H = a.H;
   const size_t head = (size_t)b * H + h;
   const int q = qt * AQB + wave * 16 + lr;
+  // positions of this sequence held in Q / K / V^T: all L, or (packed rows) up to its last
+  // valid token; keys and queries past them are zero / not written
+  const int Lk = a.seq_off ? a.seq_off[b + 1] - a.seq_off[b] : L;
+  const size_t orow = a.seq_off ? (size_t)a.seq_off[b] : (size_t)b * L;
   // only valid (mask 1) queries may ask for the fixed-max pass: padding queries' outputs are
   // never used, and the pass decision must not depend on how a sequence was padded
   const bool qvalid = q < L && a.mask[(size_t)b * L + q] == 1;
@@ -60,7 +64,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
   half8 qf[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ks++) {
-    if (q < L)
+    if (q < Lk)
       qf[ks] = *(const half8*)(a.q + (head * Lp + q) * HD + ks * 32 + g * 8);
     else
       qf[ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -104,8 +108,8 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
   if (qt * AQB >= khi) {
     // every query of this block lies past the last valid key, so it is padding (mask 0):
     // its output is never used, but stays finite (zero) for the next layer's masked P.V
-    if (q < L) {
-      __half* dst = a.out + ((size_t)b * L + q) * a.D + h * HD + 4 * g;
+    if (q < Lk) {
+      __half* dst = a.out + (orow + q) * a.D + h * HD + 4 * g;
 #pragma unroll
       for (int dt = 0; dt < 4; dt++) *(uint2*)(dst + dt * 16) = uint2{0u, 0u};
     }
@@ -123,13 +127,13 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
     for (int i = 0; i < CPT; i++) {
       const int c = tid + i * NT, row = c >> 3, ch = c & 7;
       const int key = kt * AK + row;
-      kreg[i] = key < L ? *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8) : uint4{0, 0, 0, 0};
+      kreg[i] = key < Lk ? *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8) : uint4{0, 0, 0, 0};
       const int k0 = kt * AK + ch * 8;
       uint4 vv = uint4{0, 0, 0, 0};
-      if (k0 < L) {
+      if (k0 < Lk) {
         vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
-        if (k0 + 8 > L) {  // zero the keys at and past L (the buffer's padding columns)
-          const int nv = L - k0;
+        if (k0 + 8 > Lk) {  // zero the keys at and past Lk (columns never written)
+          const int nv = Lk - k0;
           vv.x &= (nv > 0 ? 0xFFFFu : 0u) | (nv > 1 ? 0xFFFF0000u : 0u);
           vv.y &= (nv > 2 ? 0xFFFFu : 0u) | (nv > 3 ? 0xFFFF0000u : 0u);
           vv.z &= (nv > 4 ? 0xFFFFu : 0u) | (nv > 5 ? 0xFFFF0000u : 0u);
@@ -260,9 +264,9 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
 
   float tot = lsum + __shfl_xor(lsum, 16);
   tot += __shfl_xor(tot, 32);
-  if (q < L) {
+  if (q < Lk) {
     const float inv = 1.f / tot;
-    __half* dst = a.out + ((size_t)b * L + q) * a.D + h * HD + 4 * g;
+    __half* dst = a.out + (orow + q) * a.D + h * HD + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
       __half2 lo = __floats2half2_rn(o[dt][0] * inv, o[dt][1] * inv);

@@ -45,6 +45,7 @@ struct GemmP {
   float* part;  // split-K partials [K/kchunk][M][N]
   const __half* w16;  // resident f16 copy of the weights [N][K], or null
   LnPrologue ln;      // LayerNorm prologue of the small-M kernel
+  const int32_t* tokrow;  // packed rows: row m is padded token tokrow[m] (null: m)
 };
 
 // GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42). The quotient
@@ -69,7 +70,8 @@ __device__ __forceinline__ floatx4 epi_operands(const GemmP& p, int m, int f) {
     return *(const floatx4*)(p.y + (size_t)m * p.N + f);
   } else if constexpr (EPI == EPI_QKV) {
     const int sec = f / p.D, e = (f - sec * p.D) & 63;
-    const int pos = m - (m / p.L) * p.L;
+    const int r = p.tokrow ? p.tokrow[m] : m;
+    const int pos = r - (r / p.L) * p.L;
     if (sec < 2) {
       const float* cr = p.rope_cos + (size_t)pos * 32 + (e >> 1);
       const float* sr = p.rope_sin + (size_t)pos * 32 + (e >> 1);
@@ -97,7 +99,8 @@ __device__ __forceinline__ void epilogue_with(const GemmP& p, int m, int f, floa
     // the position = token index (bert.go:349-353, ops_simd.go:127-137).
     const int D = p.D;
     const int sec = f / D, fi = f - sec * D, h = fi >> 6, e = fi & 63;
-    const int b = m / p.L, pos = m - b * p.L;
+    const int r = p.tokrow ? p.tokrow[m] : m;
+    const int b = r / p.L, pos = r - b * p.L;
     if (sec < 2) {
       const float c0 = o.x, s0 = o.y, c1 = o.z, s1 = o.w;
       const float a0 = v.x * c0 - v.y * s0, a1 = v.x * s0 + v.y * c0;
@@ -463,8 +466,9 @@ __device__ __forceinline__ void qkv_tile(const GemmP& p, const floatx4 (&acc)[FB
 #pragma unroll
   for (int j = 0; j < TB; j++) {
     const int m = mb + j * 16 + lr;
-    bs[j] = m / L;
-    ps[j] = m - bs[j] * L;
+    const int r = p.tokrow ? p.tokrow[min(m, M - 1)] : m;
+    bs[j] = r / L;
+    ps[j] = r - bs[j] * L;
   }
 #pragma unroll
   for (int i = 0; i < FB; i++) {
@@ -1269,6 +1273,7 @@ static GemmP make_params(const GemmArgs& a) {
   p.g = a.g;
   p.part = a.part;
   p.w16 = a.w->w16;
+  p.tokrow = a.tokrow;
   return p;
 }
 

@@ -76,6 +76,9 @@ struct GemmArgs {
   __half* g;
   // split-K partials for M <= 64: [K/256][M][N] f32
   float* part;
+  // packed rows (padding removed): row m is token tokrow[m] = b * L + position of the padded
+  // [B][L] batch; null when row m is token m
+  const int32_t* tokrow;
 };
 
 hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st);
@@ -133,12 +136,14 @@ struct AttnArgs {
   const __half* k;
   const __half* vt;
   const int32_t* mask;   // [B][L]
-  __half* out;           // [B*L][D]
+  __half* out;           // [B*L][D], or [T][D] rows seq_off[b] + q when packed
   int B, L, Lp, H, D;
+  const int32_t* seq_off;  // packed: [B+1] first row of each sequence (it has seq_off[b+1] -
+                           // seq_off[b] positions); null: sequence b is rows b*L .. b*L+L-1
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 
-hipError_t launch_pool(const float* h, const int32_t* mask, int B, int L, int D, int out_dim, float* out,
-                       hipStream_t st);
+hipError_t launch_pool(const float* h, const int32_t* mask, const int32_t* seq_off, int B, int L, int D, int out_dim,
+                       float* out, hipStream_t st);
 
 }  // namespace lle

@@ -120,7 +120,8 @@ hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, cons
 // into an LDS list, then each thread sums 4 adjacent columns with 16 row loads in flight.
 constexpr int POOL_MAXL = 8192;
 __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ mask,
-                                                   int L, int D, int out_dim, float* __restrict__ out) {
+                                                   const int32_t* __restrict__ seq_off, int L, int D, int out_dim,
+                                                   float* __restrict__ out) {
   const int b = blockIdx.x, tid = threadIdx.x;
   __shared__ double red[256];
   __shared__ __align__(16) float vals[1024];
@@ -142,7 +143,9 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
     __syncthreads();
   }
   const int count = base;
-  const float* hb = h + (size_t)b * L * D;
+  // packed rows: sequence b starts at row seq_off[b] and its kept positions all lie before
+  // seq_off[b + 1] - seq_off[b] (positions past its last valid token were dropped)
+  const float* hb = h + (size_t)(seq_off ? seq_off[b] : b * L) * D;
   const int c0 = 4 * tid;
   if (c0 < D) {
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -201,10 +204,10 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
   for (int j = tid; j < od; j += 256) out[(size_t)b * od + j] = vals[j];
 }
 
-hipError_t launch_pool(const float* h, const int32_t* mask, int B, int L, int D, int out_dim, float* out,
-                       hipStream_t st) {
+hipError_t launch_pool(const float* h, const int32_t* mask, const int32_t* seq_off, int B, int L, int D, int out_dim,
+                       float* out, hipStream_t st) {
   if (L > POOL_MAXL || D > 1024 || D % 4) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(pool_kernel, dim3(B), dim3(256), 0, st, h, mask, L, D, out_dim, out);
+  hipLaunchKernelGGL(pool_kernel, dim3(B), dim3(256), 0, st, h, mask, seq_off, L, D, out_dim, out);
   return hipGetLastError();
 }
 

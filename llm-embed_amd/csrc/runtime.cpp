@@ -89,10 +89,11 @@ struct lle_model {
   __half *q = nullptr, *k = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
   float* part = nullptr;
   int32_t *ids = nullptr, *mask = nullptr, *status = nullptr;
+  int32_t *tokrow = nullptr, *seq_off = nullptr;  // packed-row tables of host-pointer batches
   float* out = nullptr;
-  // HIP graphs of small forwards, keyed by shape, pointers and stream
+  // HIP graphs of small forwards, keyed by shape, rows, pointers and stream
   struct GraphEntry {
-    int B, L, out_dim;
+    int B, L, T, out_dim;
     const void *ids, *mask;
     void* out;
     hipStream_t st;
@@ -124,11 +125,11 @@ static void clear_graphs(lle_model* m) {
 
 static void ws_free(lle_model* m) {
   clear_graphs(m);
-  void* bufs[] = {m->h, m->h2, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->out};
+  void* bufs[] = {m->h, m->h2, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->tokrow, m->seq_off, m->out};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   m->h = nullptr; m->h2 = nullptr; m->h16 = nullptr; m->q = m->k = m->vt = m->attn = m->ff = nullptr;
-  m->part = nullptr; m->ids = m->mask = nullptr; m->out = nullptr;
+  m->part = nullptr; m->ids = m->mask = m->tokrow = m->seq_off = nullptr; m->out = nullptr;
   m->ws_T = m->ws_heads = m->ws_part = 0;
   m->ws_B = 0;
 }
@@ -144,14 +145,16 @@ static void ws_free(lle_model* m) {
     ptr = (decltype(ptr))p_;                                                            \
   } while (0)
 
-// Grow-only workspace for a [B][L] batch.
-static int ensure_ws(lle_model* m, int B, int L) {
+// Grow-only workspace for a [B][L] batch whose forward runs on `rows` token rows (B*L, or fewer
+// when padding is packed away).
+static int ensure_ws(lle_model* m, int B, int L, int64_t rows = -1) {
   const size_t T = (size_t)B * L;
   const int Lp = (L + 63) / 64 * 64;
   const size_t heads = (size_t)B * m->H * Lp * 64;
   auto nch = [](int K) { return (size_t)(K % 768 == 0 ? K / 768 : K / 256); };
   const size_t kd = nch(m->D), kf = nch(m->F);
-  const size_t part = T <= 64 ? (size_t)64 * std::max({kd * 3 * m->D, kd * 2 * m->F, kf * m->D}) : 0;
+  const size_t R = rows < 0 ? T : (size_t)rows;
+  const size_t part = R <= 64 ? (size_t)64 * std::max({kd * 3 * m->D, kd * 2 * m->F, kf * m->D}) : 0;
   if (T <= m->ws_T && heads <= m->ws_heads && part <= m->ws_part && B <= m->ws_B) return LLE_OK;
   const size_t nT = std::max(T, m->ws_T), nH = std::max(heads, m->ws_heads), nP = std::max(part, m->ws_part);
   const int nB = std::max(B, m->ws_B);
@@ -168,6 +171,8 @@ static int ensure_ws(lle_model* m, int B, int L) {
   if (nP) WS_ALLOC(m->part, nP * 4);
   WS_ALLOC(m->ids, nT * 4);
   WS_ALLOC(m->mask, nT * 4);
+  WS_ALLOC(m->tokrow, nT * 4);
+  WS_ALLOC(m->seq_off, ((size_t)nB + 1) * 4);
   WS_ALLOC(m->out, (size_t)nB * m->D * 4);
   m->ws_T = nT;
   m->ws_heads = nH;
@@ -243,11 +248,25 @@ static double wbytes(const WeightDev& w) { return (double)w.bytes; }
 
 // BertModel.Forward (internal/embed/bert.go:216-285) for B right-padded rows of length L,
 // followed (when out != nullptr) by MeanPool + L2Normalize (+ Matryoshka).
-// ids / mask / out are device pointers already placed in m's workspace or the caller's.
+// Packed rows of a padded [B][L] batch: only positions up to each sequence's last valid token
+// are computed (rows of masked positions after it never reach a valid row: attention gives them
+// weight 0 and the pool skips them). Row t is padded token tokrow[t]; sequence b owns rows
+// seq_off[b] .. seq_off[b+1]-1. A sequence with no valid token keeps all L positions (its softmax
+// is uniform over every key).
+struct Packing {
+  int T;
+  const int32_t* tokrow;
+  const int32_t* seq_off;
+};
+
+// ids / mask / out are device pointers already placed in m's workspace or the caller's; with
+// `pk`, ids are the packed rows' ids and the mask stays [B][L].
 static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim, float* d_out,
-                   hipStream_t st) {
+                   hipStream_t st, const Packing* pk = nullptr) {
   const int D = m->D, H = m->H, F = m->F;
-  const int T = B * L, Lp = (L + 63) / 64 * 64;
+  const int T = pk ? pk->T : B * L, Lp = (L + 63) / 64 * 64;
+  const int32_t* tokrow = pk ? pk->tokrow : nullptr;
+  const int32_t* seq_off = pk ? pk->seq_off : nullptr;
   {
     EmbedArgs a{d_ids, T, m->vocab, m->tok_type, m->tok, m->tok_row_bytes, m->type0, m->enw, m->enb, m->eps, D,
                 m->h, m->h16, m->status};
@@ -271,6 +290,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
       g.n_head = H;
       g.d_model = D;
       g.part = m->part;
+      g.tokrow = tokrow;
       {
         g.w = &ly.qkv;
         g.x = m->h16;
@@ -287,7 +307,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
         }
       }
       {
-        AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D};
+        AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D, seq_off};
         Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
         LAUNCH(launch_attention(a, st));
       }
@@ -320,7 +340,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
     }
     if (d_out) {
       Scope s(m, st, "pool", 0, (double)T * D * 4);
-      LAUNCH(launch_pool(m->h, d_mask, B, L, D, out_dim, d_out, st));
+      LAUNCH(launch_pool(m->h, d_mask, seq_off, B, L, D, out_dim, d_out, st));
     }
     return LLE_OK;
   }
@@ -335,6 +355,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
     g.n_head = H;
     g.d_model = D;
     g.part = m->part;
+    g.tokrow = tokrow;
     {
       g.w = &ly.qkv;
       g.x = m->h16;
@@ -345,7 +366,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
       LAUNCH(launch_gemm(g, EPI_QKV, st));
     }
     {
-      AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D};
+      AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D, seq_off};
       Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
       LAUNCH(launch_attention(a, st));
     }
@@ -373,7 +394,7 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
   }
   if (d_out) {
     Scope s(m, st, "pool", 0, (double)T * D * 4);
-    LAUNCH(launch_pool(m->h, d_mask, B, L, D, out_dim, d_out, st));
+    LAUNCH(launch_pool(m->h, d_mask, seq_off, B, L, D, out_dim, d_out, st));
   }
   return LLE_OK;
 }
@@ -384,18 +405,19 @@ constexpr int64_t GRAPH_MAX_TOKENS = 4096;
 constexpr size_t GRAPH_CACHE = 32;
 
 static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim,
-                       float* d_out, hipStream_t st) {
+                       float* d_out, hipStream_t st, const Packing* pk = nullptr) {
+  const int T = pk ? pk->T : B * L;
   if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS)
-    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st);
+    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   for (auto& g : m->graphs)
-    if (g.B == B && g.L == L && g.out_dim == out_dim && g.ids == d_ids && g.mask == d_mask && g.out == d_out &&
-        g.st == st) {
+    if (g.B == B && g.L == L && g.T == T && g.out_dim == out_dim && g.ids == d_ids && g.mask == d_mask &&
+        g.out == d_out && g.st == st) {
       LLE_HIP(hipGraphLaunch(g.exec, st));
       return LLE_OK;
     }
   hipGraph_t graph = nullptr;
   LLE_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-  const int rc = forward(m, d_ids, d_mask, B, L, out_dim, d_out, st);
+  const int rc = forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   const hipError_t e = hipStreamEndCapture(st, &graph);
   hipGraphExec_t exec = nullptr;
   if (rc == LLE_OK && e == hipSuccess && graph &&
@@ -405,7 +427,7 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
       (void)hipGraphExecDestroy(m->graphs.front().exec);
       m->graphs.erase(m->graphs.begin());
     }
-    m->graphs.push_back({B, L, out_dim, d_ids, d_mask, d_out, st, exec});
+    m->graphs.push_back({B, L, T, out_dim, d_ids, d_mask, d_out, st, exec});
     LLE_HIP(hipGraphLaunch(exec, st));
     return LLE_OK;
   }
@@ -413,7 +435,7 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
   if (graph) (void)hipGraphDestroy(graph);
   (void)hipGetLastError();
   m->use_graphs = false;
-  return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st);
+  return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
 }
 
 static int check_batch(lle_model* m, int B, int L) {
@@ -435,31 +457,65 @@ static int check_ids(lle_model* m, const int32_t* ids, int64_t n) {
   return LLE_OK;
 }
 
-// Host-pointer batch: H2D, forward, D2H, sync.
+// Host-pointer batch: H2D, forward, D2H, sync. Embeddings (not hidden states) run on packed
+// rows when the mask has positions after a sequence's last valid token: those rows are dropped
+// before the first kernel, so the GEMMs see only the rows that can reach an embedding.
 static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B, int L, int out_dim, float* out,
                     float* hidden) {
   int rc = check_batch(m, B, L);
   if (rc) return rc;
   if (!ids || (!out && !hidden)) return fail(LLE_EINVAL, "null pointer");
   if ((rc = check_ids(m, ids, (int64_t)B * L))) return rc;
+  const size_t T = (size_t)B * L;
+  std::vector<int32_t> ones;
+  if (!mask) {
+    ones.assign(T, 1);
+    mask = ones.data();
+  }
+  // packed rows: sequence b keeps positions [0, last valid + 1), or all L when none is valid
+  std::vector<int32_t> pids, prow, soff;
+  if (!hidden) {
+    soff.resize((size_t)B + 1);
+    int64_t rows = 0;
+    for (int b = 0; b < B; b++) {
+      const int32_t* mr = mask + (size_t)b * L;
+      int n = L;
+      while (n > 0 && mr[n - 1] == 0) n--;
+      soff[b] = (int32_t)rows;
+      rows += n ? n : L;
+    }
+    soff[B] = (int32_t)rows;
+    if ((size_t)rows < T) {
+      pids.resize((size_t)rows);
+      prow.resize((size_t)rows);
+      for (int b = 0; b < B; b++)
+        for (int32_t t = soff[b], p = 0; t < soff[b + 1]; t++, p++) {
+          pids[t] = ids[(size_t)b * L + p];
+          prow[t] = b * L + p;
+        }
+    }
+  }
+  const bool packed = !pids.empty();
   std::lock_guard<std::mutex> lk(m->mu);
   LLE_HIP(hipSetDevice(m->device));
-  if ((rc = ensure_ws(m, B, L))) return rc;
-  const size_t T = (size_t)B * L;
+  if ((rc = ensure_ws(m, B, L, packed ? (int64_t)pids.size() : -1))) return rc;
   hipStream_t st = m->stream;
-  LLE_HIP(hipMemcpyAsync(m->ids, ids, T * 4, hipMemcpyHostToDevice, st));
-  if (mask) {
-    LLE_HIP(hipMemcpyAsync(m->mask, mask, T * 4, hipMemcpyHostToDevice, st));
+  Packing pk{(int)pids.size(), m->tokrow, m->seq_off};
+  if (packed) {
+    LLE_HIP(hipMemcpyAsync(m->ids, pids.data(), pids.size() * 4, hipMemcpyHostToDevice, st));
+    LLE_HIP(hipMemcpyAsync(m->tokrow, prow.data(), prow.size() * 4, hipMemcpyHostToDevice, st));
+    LLE_HIP(hipMemcpyAsync(m->seq_off, soff.data(), soff.size() * 4, hipMemcpyHostToDevice, st));
   } else {
-    std::vector<int32_t> ones(T, 1);
-    LLE_HIP(hipMemcpyAsync(m->mask, ones.data(), T * 4, hipMemcpyHostToDevice, st));
-    LLE_HIP(hipStreamSynchronize(st));
+    LLE_HIP(hipMemcpyAsync(m->ids, ids, T * 4, hipMemcpyHostToDevice, st));
   }
+  LLE_HIP(hipMemcpyAsync(m->mask, mask, T * 4, hipMemcpyHostToDevice, st));
   LLE_HIP(hipMemsetAsync(m->status, 0, 4, st));
-  if ((rc = run_forward(m, m->ids, m->mask, B, L, out_dim, out ? m->out : nullptr, st))) return rc;
+  if ((rc = run_forward(m, m->ids, m->mask, B, L, out_dim, out ? m->out : nullptr, st, packed ? &pk : nullptr)))
+    return rc;
   const int od = std::min(out_dim, m->D);
   if (out) LLE_HIP(hipMemcpyAsync(out, m->out, (size_t)B * od * 4, hipMemcpyDeviceToHost, st));
   if (hidden) LLE_HIP(hipMemcpyAsync(hidden, m->h, T * m->D * 4, hipMemcpyDeviceToHost, st));
+  // host buffers above (pids, prow, soff, ones) must outlive the copies
   LLE_HIP(hipStreamSynchronize(st));
   if (m->timing) collect_timing(m);
   return LLE_OK;
@@ -823,7 +879,7 @@ int32_t lle_embed_texts(lle_model* m, const lle_tokenizer* t, const char* const*
   if (prefix && prefix_len < 0) prefix_len = (int64_t)strlen(prefix);
   // the GEMMs address [tokens][d_ff] f16 with 32-bit offsets (check_batch)
   const int64_t tok_cap = INT32_MAX / (2 * (int64_t)std::max(m->F, m->D));
-  const int64_t budget = max_batch_tokens > 0 ? std::min<int64_t>(max_batch_tokens, tok_cap) : std::min<int64_t>(32768, tok_cap);
+  const int64_t budget = std::min<int64_t>(max_batch_tokens > 0 ? max_batch_tokens : 32768, tok_cap / 4);
   std::vector<std::vector<int32_t>> v;
   lle::tokenize_many(t->tok, texts, lens, n, prefix, prefix_len, m->max_seq, &v);
   // longest first; equal lengths keep input order
@@ -836,12 +892,14 @@ int32_t lle_embed_texts(lle_model* m, const lle_tokenizer* t, const char* const*
   for (int32_t i = 0; i < n;) {
     const int L = (int)v[order[i]].size();
     const int64_t cap = std::max<int64_t>(budget, L);
-    // a batch ends at the token budget, or, once it holds 4096 padded tokens (a forward's
-    // fixed cost is worth ~1-2k tokens), at the first text shorter than half its longest
+    // the forward packs padding away (run_host), so a batch is cut at `budget` valid tokens;
+    // its padded [B][L] tables stay within 4 x budget (buffers, 32-bit offsets)
     int32_t j = i + 1;
-    while (j < n && (int64_t)(j - i + 1) * L <= cap &&
-           !((int64_t)(j - i) * L >= 4096 && 2 * (int64_t)v[order[j]].size() < L))
+    int64_t valid = L;
+    while (j < n && valid + (int64_t)v[order[j]].size() <= cap && (int64_t)(j - i + 1) * L <= 4 * cap) {
+      valid += (int64_t)v[order[j]].size();
       j++;
+    }
     const int B = j - i;
     ids.assign((size_t)B * L, 0);
     mask.assign((size_t)B * L, 0);

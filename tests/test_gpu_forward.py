@@ -196,3 +196,35 @@ def test_graph_replay_matches_eager(gpu, small_spec):
         assert np.array_equal(bits(e.embed(b)), bits(eb))
         assert np.array_equal(bits(e.embed_padded(big_ids, np.ones_like(big_ids))), bits(big))
     compare(e.embed(a), o.embed(a), "graph replay")
+
+
+@pytest.mark.parametrize("B,L,seed", [(3, 8, 1), (4, 20, 2), (5, 40, 3), (12, 100, 4), (20, 128, 5)])
+def test_packed_rows_equal_padded_forward(gpu, small_spec, B, L, seed):
+    """lle_embed_batch (host pointers) drops the positions after each row's last valid token;
+    lle_embed_batch_async (device pointers) computes every position. The embeddings must agree
+    bit for bit, across the small fused (<= 16 rows), split-K (<= 64), decoding (< 1024) and
+    LDS-DMA (>= 1024) GEMM paths that the two row counts select."""
+    from llmembed import _hip
+    from llmembed._lib import check, lib
+
+    e, o = models(small_spec, "Q8_0")
+    D = small_spec.d_model
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, small_spec.vocab, (B, L)).astype(np.int32)
+    mask = np.zeros((B, L), np.int32)
+    for b in range(B):
+        mask[b, :int(rng.integers(1, L + 1))] = 1
+    mask[0, :] = 0                      # no valid token: kept whole (uniform softmax over L keys)
+    mask[1, :] = 1                      # no padding
+    mask[2, :] = 0                      # interior zeros, valid token at the end of a long gap
+    mask[2, [0, L // 2, L - 2]] = 1
+    print(f"packed: B={B} L={L} rows {int(sum(L if not r.any() else np.nonzero(r)[0][-1] + 1 for r in mask))}"
+          f" of {B * L}", flush=True)
+    host = e.embed_padded(ids, mask)
+    di, dm = _hip.DeviceBuffer.from_array(ids), _hip.DeviceBuffer.from_array(mask)
+    do = _hip.DeviceBuffer(B * D * 4)
+    check(lib().lle_embed_batch_async(e.model().h, di.ptr, dm.ptr, B, L, D, do.ptr, None))
+    _hip.synchronize()
+    dev = do.download((B, D), np.float32)
+    assert np.array_equal(bits(host), bits(dev))
+    compare(host[1:], o.embed_batch(ids[1:], mask[1:]), f"packed B={B} L={L}")
