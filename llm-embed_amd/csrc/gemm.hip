@@ -48,17 +48,22 @@ struct GemmP {
   const int32_t* tokrow;  // packed rows: row m is padded token tokrow[m] (null: m)
 };
 
-// GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42). The quotient
-// uses the hardware reciprocal (v_rcp_f32, 1 ulp) instead of a correctly rounded division: the
-// division sequence was a third of the up/gate GEMM's epilogue, and the result is rounded to
-// f16 right after (2^-11), so the difference (~2^-23 relative in tanh) almost never shows.
+// GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42):
+//   t = 0.7978845608 v (1 + 0.044715 v v),  tanh ~ t (27 + t^2) / (27 + 9 t^2),  +-1 past |t| 4.97,
+//   0.5 v (1 + tanh).
+// Written for the up/gate GEMM's epilogue, which runs it on 100 M values per launch with the
+// matrix cores idle: the quotient uses the hardware reciprocal (v_rcp_f32, 1 ulp) instead of a
+// correctly rounded division, three of the multiply-adds are fused, and the clamp is a select
+// (a branch per value before). Each changes the result by an ulp or so of f32 before it is
+// rounded to f16 (2^-11); every GEMM path calls this one function, so they stay bit-identical.
 __device__ __forceinline__ float gelu_r(float v) {
-  const float t = 0.7978845608f * v * (1.0f + 0.044715f * v * v);
+  const float t = (0.7978845608f * v) * fmaf(0.044715f * v, v, 1.0f);
   const float t2 = t * t;
-  float th = t * (27.0f + t2) * __builtin_amdgcn_rcpf(27.0f + 9.0f * t2);
-  if (t > 4.97f) th = 1.0f;
-  else if (t < -4.97f) th = -1.0f;
-  return 0.5f * v * (1.0f + th);
+  float r = t * (27.0f + t2) * __builtin_amdgcn_rcpf(fmaf(9.0f, t2, 27.0f));
+  asm("" : "+v"(r));  // computed for every value: otherwise the select becomes a branch around it
+  const float th = fabsf(t) > 4.97f ? copysignf(1.0f, t) : r;
+  const float hv = 0.5f * v;
+  return fmaf(hv, th, hv);
 }
 
 // Operands an epilogue reads from memory for features f..f+3 of token m: the residual
@@ -452,24 +457,54 @@ __device__ __forceinline__ void st_b16(__amdgpu_buffer_rsrc_t r, int off, __half
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, off, 0, 0);
 }
 
-// The QKV epilogue of a large-GEMM wave tile (features fb.., tokens mb..): the arithmetic of
-// epilogue_with<EPI_QKV>, with the section / head split done once per 16-feature fragment (the
-// fragment lies inside one head: D % 64 == 0), the (sequence, position) split once per token
-// fragment, and 32-bit buffer offsets instead of 64-bit pointers.
-template <int FB, int TB>
-__device__ __forceinline__ void qkv_tile(const GemmP& p, const floatx4 (&acc)[FB][TB], const floatx4 (&eop)[FB][TB],
-                                         int mb, int fb, int lane) {
-  const int lr = lane & 15, lg = lane >> 4;
-  const int D = p.D, L = p.L, Lp = p.Lp, H = p.H, M = p.M;
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q), rk = make_rsrc(p.k), rv = make_rsrc(p.vt);
-  int bs[TB], ps[TB];
+// Sequence and position of the token rows mb + j*16 + (lane & 15) of a QKV wave tile, computed
+// once per tile for both the RoPE operand loads and the stores (rows past M use row M-1; their
+// results are never stored).
+template <int TB>
+__device__ __forceinline__ void qkv_rows(const GemmP& p, int mb, int lane, int (&bs)[TB], int (&ps)[TB]) {
 #pragma unroll
   for (int j = 0; j < TB; j++) {
-    const int m = mb + j * 16 + lr;
-    const int r = p.tokrow ? p.tokrow[min(m, M - 1)] : m;
-    bs[j] = r / L;
-    ps[j] = r - bs[j] * L;
+    const int m = min(mb + j * 16 + (lane & 15), p.M - 1);
+    const int r = p.tokrow ? p.tokrow[m] : m;
+    bs[j] = r / p.L;
+    ps[j] = r - bs[j] * p.L;
   }
+}
+
+// The RoPE cos/sin pairs of epi_operands<EPI_QKV> for a wave tile: the section of each 16-feature
+// fragment (wave-uniform: fb is) is decided once per fragment, the position once per token row.
+template <int FB, int TB>
+__device__ __forceinline__ void qkv_rope_operands(const GemmP& p, const int (&ps)[TB], int fb, int lane,
+                                                  floatx4 (&eop)[FB][TB]) {
+  const int D = p.D, lg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < FB; i++) {
+    const int f0 = fb + i * 16;
+    const int sec = f0 >= 2 * D ? 2 : (f0 >= D ? 1 : 0);
+    const int e = (f0 - sec * D + lg * 4) & 63;
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      if (sec < 2) {
+        const float2 c = *(const float2*)(p.rope_cos + ps[j] * 32 + (e >> 1));
+        const float2 sn = *(const float2*)(p.rope_sin + ps[j] * 32 + (e >> 1));
+        eop[i][j] = floatx4{c.x, sn.x, c.y, sn.y};
+      } else {
+        eop[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+}
+
+// The QKV epilogue of a large-GEMM wave tile (features fb.., tokens mb..): the arithmetic of
+// epilogue_with<EPI_QKV>, with the section / head split done once per 16-feature fragment (the
+// fragment lies inside one head: D % 64 == 0), the (sequence, position) of each token row from
+// qkv_rows, and 32-bit buffer offsets instead of 64-bit pointers.
+template <int FB, int TB>
+__device__ __forceinline__ void qkv_tile(const GemmP& p, const floatx4 (&acc)[FB][TB], const floatx4 (&eop)[FB][TB],
+                                         const int (&bs)[TB], const int (&ps)[TB], int mb, int fb, int lane) {
+  const int lr = lane & 15, lg = lane >> 4;
+  const int D = p.D, Lp = p.Lp, H = p.H, M = p.M;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q), rk = make_rsrc(p.k), rv = make_rsrc(p.vt);
 #pragma unroll
   for (int i = 0; i < FB; i++) {
     const int f0 = fb + i * 16;  // wave-uniform
@@ -499,6 +534,65 @@ __device__ __forceinline__ void qkv_tile(const GemmP& p, const floatx4 (&acc)[FB
   }
 }
 
+// LDS rows are 64 bytes (4 chunks of 16 B); chunk c of row r sits at c ^ swr(r), which spreads
+// a 16-row fragment read over all banks.
+__device__ __forceinline__ int swr(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+// Epilogue of one LDS-DMA wave tile (tokens mb.., features fb..): the QKV scatter, or the
+// per-fragment epilogue of the other EPIs on the chunk total (MULTI) or 0 + the single chunk.
+template <int EPI, bool MULTI, int FB, int TB, int TF, int TT, int PF, int PT, int QT>
+__device__ __forceinline__ void tile_epilogue(const GemmP& p, const floatx4 (&acc)[FB][TB],
+                                              const floatx4 (&tot)[TF][TT], const floatx4 (&eop)[PF][PT],
+                                              const int (&qb)[QT], const int (&qp)[QT], int mb, int fb, int lane) {
+  if constexpr (EPI == EPI_QKV && !MULTI) {
+    qkv_tile<FB, TB>(p, acc, eop, qb, qp, mb, fb, lane);
+  } else {
+    const int lr = lane & 15;
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      const int m = mb + j * 16 + lr;
+      if (m < p.M) {
+#pragma unroll
+        for (int i = 0; i < FB; i++) {
+          floatx4 v;
+          if constexpr (MULTI) {
+            v = tot[i][j];
+          } else {
+            v = floatx4{0.f, 0.f, 0.f, 0.f};
+            v += acc[i][j];  // total = 0 + chunk, as the split-K reduction computes it
+          }
+          if constexpr (EPI == EPI_QKV)
+            epilogue_with<EPI>(p, m, fb + i * 16 + (lane >> 4) * 4, v, eop[i][j]);
+          else
+            epilogue<EPI>(p, m, fb + i * 16 + (lane >> 4) * 4, v);
+        }
+      }
+    }
+  }
+}
+
+// XCD-aware tile order of the LDS-DMA kernels (as gemm_big's): workgroup b runs on XCD b % 8,
+// so the tile grid is cut into MG x NG shares, one per XCD, each walked N-fastest; concurrently
+// running tiles of one XCD then share their X and W rows in its L2.
+template <int BM, int BN>
+__device__ __forceinline__ void xcd_tile(int& m0, int& n0) {
+  constexpr int NG = BN >= 256 ? 2 : 1, MG = 8 / NG;
+  const int nt = gridDim.x, mt = gridDim.y, G = nt * mt;
+  const int b = blockIdx.x + blockIdx.y * nt, xcd = b & 7, slot = b >> 3;
+  n0 = blockIdx.x * BN;
+  m0 = blockIdx.y * BM;
+  if (nt % NG == 0 && mt % MG == 0) {
+    const int ntl = nt / NG, mtl = mt / MG;
+    n0 = ((xcd % NG) * ntl + slot % ntl) * BN;
+    m0 = ((xcd / NG) * mtl + slot / ntl) * BM;
+  } else if (NG == 1) {
+    const int q = G >> 3, r = G & 7;
+    const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+    n0 = (t % nt) * BN;
+    m0 = (t / nt) * BM;
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int NS, int EPI, bool MULTI>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   constexpr int NW = WM * WN;
@@ -524,23 +618,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  {
-    // the same XCD-aware tile order as gemm_big
-    constexpr int NG = BN >= 256 ? 2 : 1, MG = 8 / NG;
-    const int nt = gridDim.x, mt = gridDim.y, G = nt * mt;
-    const int b = blockIdx.x + blockIdx.y * nt, xcd = b & 7, slot = b >> 3;
-    if (nt % NG == 0 && mt % MG == 0) {
-      const int ntl = nt / NG, mtl = mt / MG;
-      n0 = ((xcd % NG) * ntl + slot % ntl) * BN;
-      m0 = ((xcd / NG) * mtl + slot / ntl) * BM;
-    } else if (NG == 1) {
-      const int q = G >> 3, r = G & 7;
-      const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-      n0 = (t % nt) * BN;
-      m0 = (t / nt) * BM;
-    }
-  }
+  int m0, n0;
+  xcd_tile<BM, BN>(m0, n0);
   const int M = p.M, K = p.K;
   const int KT = K / KSTEP;
   const int steps_per_chunk = kchunk_of(K) / KSTEP;
@@ -563,13 +642,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   // which counts on every older memory operation being complete). Rows past M load row M-1.
   constexpr bool PRE = EPI == EPI_QKV;
   floatx4 eop[PRE ? FB : 1][PRE ? TB : 1];
+  int qb[PRE ? TB : 1], qp[PRE ? TB : 1];
   if constexpr (PRE) {
-#pragma unroll
-    for (int j = 0; j < TB; j++)
-#pragma unroll
-      for (int i = 0; i < FB; i++)
-        eop[i][j] = epi_operands<EPI>(p, min(m0 + wm * TM + j * 16 + (lane & 15), M - 1),
-                                      n0 + wn * TN + i * 16 + (lane >> 4) * 4);
+    qkv_rows<TB>(p, m0 + wm * TM, lane, qb, qp);
+    qkv_rope_operands<FB, TB>(p, qp, n0 + wn * TN, lane, eop);
   }
 
   // loop-invariant byte offsets; the K step advances in the scalar offset. Rows past M re-read
@@ -660,30 +736,38 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     }
   }
 
-  if constexpr (EPI == EPI_QKV && !MULTI) {
-    qkv_tile<FB, TB>(p, acc, eop, m0 + wm * TM, n0 + wn * TN, lane);
-    return;
-  }
+  if constexpr (EPI == EPI_GEGLU && BM == 256 && BN == 256 && WM == 4 && WN == 2 && !MULTI) {
+    // GeGLU outputs go through LDS so that every global store is a full 16-byte chunk of a row
+    // (8 lanes per 128-byte line): stored straight from the MFMA layout, each instruction wrote
+    // 16 rows x 16 bytes and the stores took a sixth of the kernel. The 256 x 128 f16 tile
+    // sits in the two X stages (rows 0-127, 128-255), chunk c of row r at c ^ (r & 15).
+    typedef _Float16 ORow[128];
+    static_assert(sizeof(sX0) == 128 * sizeof(ORow) && sizeof(sX1) == 128 * sizeof(ORow), "staging");
+    __syncthreads();  // every wave is done reading the last stage
+    ORow* so = (ORow*)(wm < 2 ? &sX0[0][0] : &sX1[0][0]);
 #pragma unroll
-  for (int j = 0; j < TB; j++) {
-    const int m = m0 + wm * TM + j * 16 + lr;
-    if (m < M) {
+    for (int j = 0; j < TB; j++) {
+      const int r = (wm & 1) * 64 + j * 16 + lr;
 #pragma unroll
       for (int i = 0; i < FB; i++) {
-        floatx4 v;
-        if constexpr (MULTI) {
-          v = tot[i][j];
-        } else {
-          v = floatx4{0.f, 0.f, 0.f, 0.f};
-          v += acc[i][j];  // total = 0 + chunk, as the split-K reduction computes it
-        }
-        if constexpr (PRE)
-          epilogue_with<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, v, eop[i][j]);
-        else
-          epilogue<EPI>(p, m, n0 + wn * TN + i * 16 + (lane >> 4) * 4, v);
+        floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+        v += acc[i][j];  // total = 0 + chunk, as epilogue<EPI_GEGLU> receives it
+        const float o0 = gelu_r(v.y) * v.x, o1 = gelu_r(v.w) * v.z;
+        *(__half2*)&so[r][((wn * 8 + i) ^ (r & 15)) * 8 + lg * 2] = __floats2half2_rn(o0, o1);
       }
     }
+    __syncthreads();
+    const int F = p.N >> 1;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int q = tid + k * 512, row = q >> 4, c = q & 15, rr = row & 127;
+      const ORow* src = (const ORow*)(row < 128 ? &sX0[0][0] : &sX1[0][0]);
+      const uint4 val = *(const uint4*)&src[rr][(c ^ (rr & 15)) * 8];
+      if (m0 + row < M) *(uint4*)(p.g + (size_t)(m0 + row) * F + (n0 >> 1) + c * 8) = val;
+    }
+    return;
   }
+  tile_epilogue<EPI, MULTI, FB, TB>(p, acc, tot, eop, qb, qp, m0 + wm * TM, n0 + wn * TN, lane);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -693,9 +777,6 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
 // the whole 768-row weight step is 48 KB of LDS, double-buffered. The per-accumulator MFMA
 // sequence, the chunk totals, the residual add and ln_row are those of gemm_big + ln_kernel,
 // so every output bit equals that path's (and the small-M path's).
-// LDS rows are 64 bytes (4 chunks of 16 B); chunk c of row r sits at c ^ swr(r), which spreads
-// a 16-row fragment read over all banks.
-__device__ __forceinline__ int swr(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 
 constexpr int LN_N = 768, LN_KS = 32, LN_RS = LN_N + 4;  // LN staging row stride (floats)
 
