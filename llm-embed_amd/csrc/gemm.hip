@@ -600,20 +600,13 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   constexpr int XI = BM / 8 / NW, WI = BN / 8 / NW;  // 1-KB loads per wave per K step
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows per wave");
   static_assert(NS == 2 || NS == 3, "stages");
-  // one LDS object per stage: the compiler's wait-count pass then knows that reading one stage
-  // does not depend on the LDS-DMA loads still flying into another
-  __shared__ __attribute__((aligned(1024))) _Float16 sW0[BN][KSTEP], sW1[BN][KSTEP], sW2[NS > 2 ? BN : 1][KSTEP];
-  __shared__ __attribute__((aligned(1024))) _Float16 sX0[BM][KSTEP], sX1[BM][KSTEP], sX2[NS > 2 ? BM : 1][KSTEP];
-  auto stW = [&](auto S) -> _Float16(*)[KSTEP] {
-    if constexpr (decltype(S)::value == 0) return sW0;
-    else if constexpr (decltype(S)::value == 1) return sW1;
-    else return sW2;
-  };
-  auto stX = [&](auto S) -> _Float16(*)[KSTEP] {
-    if constexpr (decltype(S)::value == 0) return sX0;
-    else if constexpr (decltype(S)::value == 1) return sX1;
-    else return sX2;
-  };
+  // NS stages of [BM X rows | BN W rows] x 128 bytes in one LDS array (stage offsets are
+  // compile-time constants); after the K loop the array stages the epilogue's tile
+  constexpr int X_STAGE = BM * KSTEP * 2, STAGE = X_STAGE + BN * KSTEP * 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
+  typedef _Float16 KRow[KSTEP];
+  auto stX = [&](auto S) { return (KRow*)(smem + decltype(S)::value * STAGE); };
+  auto stW = [&](auto S) { return (KRow*)(smem + decltype(S)::value * STAGE + X_STAGE); };
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -663,8 +656,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     wo[j] = ((n0 + r) * K + c * 8) * 2;
   }
   auto issue = [&](auto S, int kt) {
-    _Float16(*sx)[KSTEP] = stX(S);
-    _Float16(*sw)[KSTEP] = stW(S);
+    KRow* sx = stX(S);
+    KRow* sw = stW(S);
 #pragma unroll
     for (int j = 0; j < XI; j++) dma16(rx, &sx[(wave + j * NW) * 8][0], xo[j], kt * KSTEP * 2);
 #pragma unroll
@@ -672,8 +665,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   };
   const int lr = lane & 15, lg = lane >> 4;
   auto compute = [&](auto S, int kt) {
-    const _Float16(*sw)[KSTEP] = stW(S);
-    const _Float16(*sx)[KSTEP] = stX(S);
+    const KRow* sw = stW(S);
+    const KRow* sx = stX(S);
     half8 af[2][FB], bf[2][TB];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
@@ -739,12 +732,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   if constexpr (EPI == EPI_GEGLU && BM == 256 && BN == 256 && WM == 4 && WN == 2 && !MULTI) {
     // GeGLU outputs go through LDS so that every global store is a full 16-byte chunk of a row
     // (8 lanes per 128-byte line): stored straight from the MFMA layout, each instruction wrote
-    // 16 rows x 16 bytes and the stores took a sixth of the kernel. The 256 x 128 f16 tile
-    // sits in the two X stages (rows 0-127, 128-255), chunk c of row r at c ^ (r & 15).
+    // 16 rows x 16 bytes and the stores took a sixth of the kernel. The 256 x 128 f16 tile:
+    // chunk c of row r at c ^ (r & 15) (the low bits of a 16-row fragment's row).
     typedef _Float16 ORow[128];
-    static_assert(sizeof(sX0) == 128 * sizeof(ORow) && sizeof(sX1) == 128 * sizeof(ORow), "staging");
+    static_assert(sizeof(smem) >= 256 * sizeof(ORow), "staging");
     __syncthreads();  // every wave is done reading the last stage
-    ORow* so = (ORow*)(wm < 2 ? &sX0[0][0] : &sX1[0][0]);
+    ORow* so = (ORow*)smem + (wm >> 1) * 128;
 #pragma unroll
     for (int j = 0; j < TB; j++) {
       const int r = (wm & 1) * 64 + j * 16 + lr;
@@ -761,9 +754,54 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       const int q = tid + k * 512, row = q >> 4, c = q & 15, rr = row & 127;
-      const ORow* src = (const ORow*)(row < 128 ? &sX0[0][0] : &sX1[0][0]);
-      const uint4 val = *(const uint4*)&src[rr][(c ^ (rr & 15)) * 8];
+      const uint4 val = *(const uint4*)&((const ORow*)smem)[row][(c ^ (rr & 15)) * 8];
       if (m0 + row < M) *(uint4*)(p.g + (size_t)(m0 + row) * F + (n0 >> 1) + c * 8) = val;
+    }
+    return;
+  }
+  if constexpr (EPI == EPI_RESID && BM == 256 && BN == 128 && WM == 4 && WN == 2) {
+    // h += X W^T through LDS: the f32 tile totals are staged (row r's 16-byte chunk c at
+    // c ^ (r & 31)), then each thread reads 16 bytes of residual, adds and stores whole row chunks
+    // (32 lanes per 512-byte row) instead of 16 rows x 64 bytes per instruction.
+    typedef float TRow[128];
+    static_assert(sizeof(smem) >= 256 * sizeof(TRow), "staging");
+    __syncthreads();  // every wave is done reading the last stage
+    TRow* so = (TRow*)smem;
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      const int r = wm * 64 + j * 16 + lr;
+#pragma unroll
+      for (int i = 0; i < FB; i++) {
+        floatx4 v;
+        if constexpr (MULTI) {
+          v = tot[i][j];
+        } else {
+          v = floatx4{0.f, 0.f, 0.f, 0.f};
+          v += acc[i][j];  // total = 0 + chunk, as the split-K reduction computes it
+        }
+        *(floatx4*)&so[r][((wn * 16 + i * 4 + lg) ^ (r & 31)) * 4] = v;
+      }
+    }
+    __syncthreads();
+    const int N = p.N;
+#pragma unroll
+    for (int k0 = 0; k0 < 16; k0 += 8) {
+      floatx4 res[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {  // residual loads first: one round trip for 8 chunks
+        const int q = tid + (k0 + k) * 512, row = q >> 5, c = q & 31;
+        res[k] = m0 + row < M ? *(const floatx4*)(p.y + (size_t)(m0 + row) * N + n0 + c * 4)
+                              : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int q = tid + (k0 + k) * 512, row = q >> 5, c = q & 31;
+        const floatx4 v = *(const floatx4*)&so[row][(c ^ (row & 31)) * 4];
+        // hiddens[i][j] += out[i][j]  (internal/embed/bert.go:262-264, 276-278)
+        floatx4 h = res[k];
+        h.x = h.x + v.x; h.y = h.y + v.y; h.z = h.z + v.z; h.w = h.w + v.w;
+        if (m0 + row < M) *(floatx4*)(p.y + (size_t)(m0 + row) * N + n0 + c * 4) = h;
+      }
     }
     return;
   }
