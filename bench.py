@@ -255,6 +255,50 @@ def main():
         extras["config3_Q4_K_M"] = run_cfg(3, "Q4_K_M", 10)
         extras["config5_Q8_0"] = run_cfg(5, "Q8_0", 5)
 
+        # Config 2: the isolated quantised projections Y = X W^T at the encoder's four shapes,
+        # M in {8, 512, 32768}, four formats; X f16 resident on the device (lle_gemm_f16_async),
+        # device time per call from HIP events (median of 20). Roofline: the dense fp16 MFMA peak
+        # for FLOP/s, and for bytes the quantised W + X f16 + Y f32 read/written once.
+        from llmembed import quant as q_
+
+        c2 = []
+        rng2 = np.random.default_rng(0xC2)
+        xbuf = _hip.DeviceBuffer(32768 * 3072 * 2)
+        ybuf = _hip.DeviceBuffer(32768 * 3072 * 4)
+        pbuf = _hip.DeviceBuffer(4 * 1024 * 3072 * 4)  # split-K partials below 1024 rows
+        xbuf_h = (rng2.standard_normal(32768 * 3072) * 1.0).astype(np.float16)
+        xbuf.upload(xbuf_h)
+        e0, e1 = _hip.Event(), _hip.Event()
+        for tname, t in (("Q8_0", q_.Q8_0), ("Q6_K", q_.Q6_K), ("Q5_K", q_.Q5_K), ("Q4_K", q_.Q4_K)):
+            for K_c, N_c in ((768, 2304), (768, 768), (768, 3072), (3072, 768)):
+                wq = q_.quantize(t, (rng2.standard_normal((N_c, K_c)) * 0.02).astype(np.float32), rng2)
+                W = llmembed.Weight(t, wq, K_c, N_c)
+                for M_c in (8, 512, 32768):
+                    def call():
+                        W.gemm_f16_async(xbuf.value, M_c, ybuf.value, pbuf.value if M_c < 1024 else 0, stream.h.value)
+                    for _ in range(3):
+                        call()
+                    ts = []
+                    for _ in range(20):
+                        e0.record(stream)
+                        call()
+                        e1.record(stream)
+                        ts.append(e0.elapsed_ms(e1))
+                    ms = float(np.median(ts))
+                    flops = 2.0 * M_c * N_c * K_c
+                    nbytes = float(wq.nbytes) + M_c * K_c * 2 + M_c * N_c * 4
+                    c2.append(dict(fmt=tname, K=K_c, N=N_c, M=M_c, us=1e3 * ms, tflops=flops / ms / 1e9,
+                                   mfma_frac=flops / ms / 1e9 / PEAK_F16_TFLOPS, gbs=nbytes / ms / 1e6,
+                                   hbm_frac=nbytes / ms / 1e6 / PEAK_HBM_GBS))
+                W.close()
+        extras["config2"] = c2
+        for r in c2:
+            if r["fmt"] in ("Q8_0", "Q4_K"):
+                log(f"[bench] config 2 {r['fmt']:4s} K={r['K']:4d} N={r['N']:4d} M={r['M']:5d}: {r['us']:8.1f} us "
+                    f"{r['tflops']:7.1f} TFLOP/s ({100 * r['mfma_frac']:4.1f}% MFMA) {r['gbs']:7.0f} GB/s "
+                    f"({100 * r['hbm_frac']:4.1f}% HBM)")
+        del xbuf, ybuf, pbuf
+
         # Text path (EmbedBatch over strings): native host tokeniser, then lle_embed_texts'
         # length-ordered batches, against the same texts in input order, 256 per padded batch.
         corpus = synth.texts(4096, seed=0x7E57, min_words=4, max_words=110)

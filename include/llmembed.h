@@ -161,6 +161,13 @@ int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y);
 /* Device pointers: X f32 [M][K] is converted to f16 into d_x16 (M*K halfs, caller-owned),
  * then Y f32 [M][N]; enqueued on stream. */
 int32_t lle_gemm_async(const lle_weight* w, const float* d_X, void* d_x16, int32_t M, float* d_Y, void* stream);
+/* The same projection on activations already held as f16 on the device (what the encoder's own
+ * kernels hand each other): Y f32 [M][N] = X16 [M][K] . W^T, enqueued on stream. d_part is a
+ * split-K workspace of (K % 768 == 0 ? K / 768 : K / 256) * M * N floats (the 768-wide K chunks
+ * are summed in order): required for M <= 64; for 64 < M < 1024 it lets several-chunk K run on
+ * row blocks that fill the GPU (NULL: 128-row tiles); unused from 1024 rows. */
+int32_t lle_gemm_f16_async(const lle_weight* w, const void* d_x16, int32_t M, float* d_Y, float* d_part,
+                           void* stream);
 
 /* ---- Host tokeniser (no GPU use) ----------------------------------------------------------
  * WordPieceTokenizer (internal/embed/tokenizer.go:15-19): nomic's "▁"-prefixed vocabulary,

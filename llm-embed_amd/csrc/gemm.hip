@@ -1100,6 +1100,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n0 = blockIdx.x * BN, c = blockIdx.y, kbase = c * NPIECE * PK;
+  const int mb = blockIdx.z * BM;  // row block (gridDim.z > 1 for 64 < M < 1024)
   const int M = p.M, K = p.K;
 
   RawSeg wr[NP][WPT];
@@ -1115,7 +1116,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
       for (int i = 0; i < XPT; i++) {
         const int cc = tid + i * NT;
         if (cc < XCH) {
-          const int row = cc >> 5, ch = cc & 31;
+          const int row = mb + (cc >> 5), ch = cc & 31;
           xr[slot][i] = row < M ? *(const uint4*)(p.x + (size_t)row * K + kb + ch * 8) : uint4{0, 0, 0, 0};
         }
       }
@@ -1183,7 +1184,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
   if constexpr (DIRECT) {
 #pragma unroll
     for (int j = 0; j < TB; j++)
-      if (j * 16 + lr < M) eop[j] = epi_operands<EPI>(p, j * 16 + lr, n0 + wave * 16 + lg * 4);
+      if (mb + j * 16 + lr < M) eop[j] = epi_operands<EPI>(p, mb + j * 16 + lr, n0 + wave * 16 + lg * 4);
   }
   floatx4 acc[TB];
 #pragma unroll
@@ -1228,7 +1229,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
     // single-chunk K: the total is 0 + this chunk, finished here with the epilogue
 #pragma unroll
     for (int j = 0; j < TB; j++) {
-      const int m = j * 16 + lr;
+      const int m = mb + j * 16 + lr;
       if (m < M) {
         floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
         v += acc[j];
@@ -1239,7 +1240,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
     float* part = p.part + (size_t)c * M * p.N;
 #pragma unroll
     for (int j = 0; j < TB; j++) {
-      const int m = j * 16 + lr;
+      const int m = mb + j * 16 + lr;
       if (m < M) *(floatx4*)(part + (size_t)m * p.N + n0 + wave * 16 + (lane >> 4) * 4) = acc[j];
     }
   }
@@ -1258,15 +1259,17 @@ __global__ __launch_bounds__(256) void gemm_reduce(GemmP p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// M <= 64. K spanning one canonical chunk: one kernel, epilogue applied in place. Several
-// chunks: per-chunk partials, then gemm_reduce (or, when `reduce` is false, the caller's own
-// ordered reduction, e.g. the fused residual + LayerNorm row kernel).
+// M <= 64, or 64 < M < 1024 in BM-row blocks (too few tokens to fill the GPU with 128-row
+// tiles: 24 of them for a 512 x 768 output). K spanning one canonical chunk: one kernel,
+// epilogue applied in place. Several chunks: per-chunk partials (nch x M x N floats in p.part),
+// then gemm_reduce (or, when `reduce` is false, the caller's own ordered reduction, e.g. the
+// fused residual + LayerNorm row kernel).
 template <int FMT, int BM, int EPI>
 static hipError_t launch_small(const GemmP& p, hipStream_t st, bool reduce) {
   constexpr int BN = 64;  // 16-feature one-wave blocks measured no faster at M = 8
   const int kc = kchunk_of(p.K);
   const int nch = p.K / kc;
-  const dim3 grid(p.N / BN, nch), blk(BN * 4);
+  const dim3 grid(p.N / BN, nch, (p.M + BM - 1) / BM), blk(BN * 4);
   if (nch == 1) {
     if (kc == 768)
       hipLaunchKernelGGL((gemm_small<FMT, BM, BN, 3, EPI, true>), grid, blk, 0, st, p);
@@ -1322,6 +1325,7 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
     return launch_small<FMT, 64, EPI>(p, st, reduce);
   }
   const bool multi = p.K > kchunk_of(p.K);
+  if (p.M < 1024 && (!multi || p.part)) return launch_small<FMT, 64, EPI>(p, st, reduce);
   if (p.M >= 1024 && p.w16) {
     if (!multi && p.N >= 4096 && p.N % 256 == 0) {  // 2 stages of 64 KB
       dim3 grid(p.N / 256, (p.M + 255) / 256);
@@ -1456,7 +1460,7 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
     }
     return hipGetLastError();
   }
-  if (p.M <= 64 && (nch == 2 || nch == 3 || nch == 4 || nch == 8 || nch == 12)) {
+  if (p.M < 1024 && p.part && (nch == 2 || nch == 3 || nch == 4 || nch == 8 || nch == 12)) {
     hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, false);
     if (e != hipSuccess) return e;
     return launch_reduce_resid_ln(p.part, nch, p.M, p.N, p.y, p.y, h16, w, b, eps, st);

@@ -154,7 +154,8 @@ static int ensure_ws(lle_model* m, int B, int L, int64_t rows = -1) {
   auto nch = [](int K) { return (size_t)(K % 768 == 0 ? K / 768 : K / 256); };
   const size_t kd = nch(m->D), kf = nch(m->F);
   const size_t R = rows < 0 ? T : (size_t)rows;
-  const size_t part = R <= 64 ? (size_t)64 * std::max({kd * 3 * m->D, kd * 2 * m->F, kf * m->D}) : 0;
+  // split-K partials of the GEMMs below 1024 rows: chunks x rows x N floats
+  const size_t part = R < 1024 ? std::max<size_t>(R, 64) * std::max({kd * 3 * m->D, kd * 2 * m->F, kf * m->D}) : 0;
   if (T <= m->ws_T && heads <= m->ws_heads && part <= m->ws_part && B <= m->ws_B) return LLE_OK;
   const size_t nT = std::max(T, m->ws_T), nH = std::max(heads, m->ws_heads), nP = std::max(part, m->ws_part);
   const int nB = std::max(B, m->ws_B);
@@ -1045,6 +1046,23 @@ int32_t lle_gemm_async(const lle_weight* w, const float* d_X, void* d_x16, int32
   return gemm_enqueue(w, d_X, d_x16, M, d_Y, nullptr, stream ? (hipStream_t)stream : w->stream);
 }
 
+int32_t lle_gemm_f16_async(const lle_weight* w, const void* d_x16, int32_t M, float* d_Y, float* d_part,
+                           void* stream) {
+  if (!w || !d_x16 || !d_Y || M <= 0) return fail(LLE_EINVAL, "bad argument");
+  if (M <= 64 && !d_part) return fail(LLE_EINVAL, "M <= 64 needs the split-K workspace d_part");
+  if (M >= 1024) d_part = nullptr;
+  LLE_HIP(hipSetDevice(w->device));
+  GemmArgs g{};
+  g.w = &w->w;
+  g.x = (const __half*)d_x16;
+  g.M = M;
+  g.y = d_Y;
+  g.part = d_part;
+  hipStream_t st = stream ? (hipStream_t)stream : w->stream;
+  LAUNCH(launch_gemm(g, EPI_F32, st));
+  return LLE_OK;
+}
+
 int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y) {
   if (!w || !X || !Y || M <= 0) return fail(LLE_EINVAL, "bad argument");
   LLE_HIP(hipSetDevice(w->device));
@@ -1053,7 +1071,7 @@ int32_t lle_gemm(const lle_weight* w, const float* X, int32_t M, float* Y) {
   hipError_t e = hipMalloc(&dX, M * K * 4);
   if (e == hipSuccess) e = hipMalloc(&dx16, M * K * 2);
   if (e == hipSuccess) e = hipMalloc(&dY, M * N * 4);
-  if (e == hipSuccess && M <= 64) e = hipMalloc(&dP, (K % 768 == 0 ? K / 768 : K / 256) * (size_t)M * N * 4);
+  if (e == hipSuccess && M < 1024) e = hipMalloc(&dP, (K % 768 == 0 ? K / 768 : K / 256) * (size_t)M * N * 4);
   int rc = LLE_OK;
   if (e != hipSuccess) rc = fail(LLE_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
   if (!rc && hipMemcpy(dX, X, M * K * 4, hipMemcpyHostToDevice) != hipSuccess) rc = fail(LLE_EDEVICE, "copy X");

@@ -18,7 +18,7 @@ EXPORTS = [
     "lle_model_create", "lle_model_load_gguf", "lle_model_destroy", "lle_model_dims", "lle_embed",
     "lle_embed_batch", "lle_embed_batch_async", "lle_forward_hidden", "lle_model_status",
     "lle_model_set_timing", "lle_model_get_timing", "lle_weight_create", "lle_weight_destroy",
-    "lle_weight_dequant", "lle_weight_dequant_f16", "lle_gemm", "lle_gemm_async",
+    "lle_weight_dequant", "lle_weight_dequant_f16", "lle_gemm", "lle_gemm_async", "lle_gemm_f16_async",
     "lle_tokenizer_load_gguf", "lle_tokenizer_create", "lle_tokenizer_destroy", "lle_tokenizer_vocab_size",
     "lle_tokenize", "lle_tokenize_batch", "lle_embed_texts",
 ]
@@ -87,6 +87,7 @@ def lib(path: str | None = None):
         "lle_weight_dequant_f16": ([P, P], I32),
         "lle_gemm": ([P, P, I32, P], I32),
         "lle_gemm_async": ([P, P, P, I32, P, P], I32),
+        "lle_gemm_f16_async": ([P, P, I32, P, P, P], I32),
         "lle_tokenizer_load_gguf": ([C.c_char_p, C.POINTER(P)], I32),
         "lle_tokenizer_create": ([P, P, I32, C.POINTER(P)], I32),
         "lle_tokenizer_destroy": ([P], I32),
@@ -165,6 +166,13 @@ class Weight:
         Y = np.empty((M, self.N), np.float32)
         check(lib().lle_gemm(self.h, ptr(X), M, ptr(Y)))
         return Y
+
+    def part_floats(self, M: int) -> int:
+        """Split-K workspace size of lle_gemm_f16_async below 1024 rows (0 from 1024)."""
+        return ((self.K // 768) if self.K % 768 == 0 else (self.K // 256)) * M * self.N if M < 1024 else 0
+
+    def gemm_f16_async(self, d_x16: int, M: int, d_y: int, d_part: int = 0, stream: int = 0):
+        check(lib().lle_gemm_f16_async(self.h, d_x16, M, d_y, d_part or None, stream or None))
 
     def gemm_async(self, d_x: int, d_x16: int, M: int, d_y: int, stream: int = 0):
         check(lib().lle_gemm_async(self.h, C.c_void_p(d_x), C.c_void_p(d_x16), M, C.c_void_p(d_y),

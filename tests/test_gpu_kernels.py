@@ -184,3 +184,22 @@ def test_weight_errors(gpu):
         gpu.Weight(2, np.zeros(1024, np.uint8), 256, 128)  # Q4_0: not on the path
     with pytest.raises(gpu.LLEError):
         gpu.Weight(quant.Q8_0, np.zeros(34 * 10, np.uint8), 320, 1)  # N not a multiple of 128
+
+
+@pytest.mark.parametrize("t,K,N", [(quant.Q8_0, 768, 2304), (quant.Q5_K, 3072, 768), (quant.Q4_K, 768, 3072)])
+def test_gemm_f16_entry_matches_host_entry(gpu, t, K, N):
+    """lle_gemm_f16_async (f16 activations on the device, caller's split-K workspace) gives the
+    bits of lle_gemm (f32 host activations, rounded to f16 inside) at every M regime."""
+    from llmembed import _hip
+
+    for M in (8, 64, 100, 512, 1100):
+        blocks, X, _ = _gemm_case(t, K, N, M, 5 * K + N + M + t)
+        W = gpu.Weight(t, blocks, K, N)
+        ref = W.gemm(X)
+        x16 = _hip.DeviceBuffer.from_array(X.astype(np.float16))
+        dy = _hip.DeviceBuffer(M * N * 4)
+        dp = _hip.DeviceBuffer(max(W.part_floats(M), 1) * 4)
+        for part in ((dp.value,) if M <= 64 else (dp.value, 0)):  # row blocks, or 128-row tiles
+            W.gemm_f16_async(x16.value, M, dy.value, part)
+            _hip.synchronize()
+            assert np.array_equal(bits(dy.download((M, N), np.float32)), bits(ref)), (M, part)
