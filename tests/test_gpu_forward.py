@@ -228,3 +228,34 @@ def test_packed_rows_equal_padded_forward(gpu, small_spec, B, L, seed):
     dev = do.download((B, D), np.float32)
     assert np.array_equal(bits(host), bits(dev))
     compare(host[1:], o.embed_batch(ids[1:], mask[1:]), f"packed B={B} L={L}")
+
+
+@pytest.mark.parametrize("qkv_std", [0.02, 0.3])
+def test_small_batch_schedule_bitexact(gpu, small_spec, qkv_std):
+    """Batches of <= 16 rows run the small-batch schedule (LayerNorms inside the consuming GEMMs,
+    split-K partials, one-tile attention); larger batches the general one. A row must come out
+    with the same bits either way, with masked keys inside the sequence, padding, a sequence with
+    no valid token and (qkv_std 0.3) the x < -10 cutoff dropping keys."""
+    e, o = models(small_spec, "Q8_0", 101 if qkv_std != 0.02 else 100, qkv_std=qkv_std)
+    rng = np.random.default_rng(41)
+    V = small_spec.vocab
+    cases = []
+    for L in (1, 5, 12, 16):
+        ids = rng.integers(0, V, L).astype(np.int32)
+        cases.append((ids, np.ones(L, np.int32)))
+    ids = rng.integers(0, V, 14).astype(np.int32)
+    cases.append((ids, np.array([1, 1, 0, 1, 0, 0, 1, 1, 1, 0, 1, 1, 0, 0], np.int32)))  # interior + trailing zeros
+    cases.append((rng.integers(0, V, 6).astype(np.int32), np.zeros(6, np.int32)))  # no valid token
+    filler = rng.integers(0, V, (2, 40)).astype(np.int32)
+    for ids, mask in cases:
+        L = ids.size
+        print(f"small batch: L={L} valid={int(mask.sum())} qkv_std={qkv_std}", flush=True)
+        small = e.embed_padded(ids[None, :], mask[None, :])      # <= 16 rows
+        big_ids = np.zeros((3, 40), np.int32)
+        big_mask = np.zeros((3, 40), np.int32)
+        big_ids[0, :L], big_mask[0, :L] = ids, mask
+        big_ids[1:], big_mask[1:] = filler, 1
+        big = e.embed_padded(big_ids, big_mask)                  # > 16 rows
+        assert np.array_equal(bits(small[0]), bits(big[0])), (L, mask.tolist())
+        if mask.any():
+            compare(small, o.embed_batch(ids[None, :], mask[None, :]), f"small batch L={L}")
