@@ -59,6 +59,9 @@ def main():
     ap.add_argument("--probe-traffic", action="store_true",
                     help="for rocprofv3 --pmc runs: two config-4 forwards, then one 256 MiB device-to-device copy "
                          "(the calibration of FETCH_SIZE / WRITE_SIZE); prints no JSON")
+    ap.add_argument("--probe-config", type=int, default=4, choices=(3, 4, 5),
+                    help="with --probe-traffic: the configuration whose two forwards are run (padded batch, "
+                         "device-pointer entry)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); sequences are "
@@ -90,14 +93,25 @@ def main():
         check(L_.lle_embed_batch_async(model.h, d_ids.ptr, d_mask.ptr, B, L, D, d_out.ptr, stream.h))
 
     if args.probe_traffic:
-        step()
-        step()
+        if args.probe_config == 4:
+            step()
+            step()
+        else:
+            ids_p, mask_p = synth.config_inputs(args.probe_config)
+            mp = llmembed.Embedder.load(synth.model_path(spec, synth.CONFIG_MIX[args.probe_config],
+                                                         synth.CONFIG_SEED + args.probe_config)).model()
+            dip, dmp = _hip.DeviceBuffer.from_array(ids_p), _hip.DeviceBuffer.from_array(mask_p)
+            dop = _hip.DeviceBuffer(ids_p.shape[0] * D * 4)
+            for _ in range(2):
+                check(L_.lle_embed_batch_async(mp.h, dip.ptr, dmp.ptr, ids_p.shape[0], ids_p.shape[1], D, dop.ptr,
+                                               stream.h))
+            stream.synchronize()
         n = 256 << 20
         src, dst = _hip.DeviceBuffer(n), _hip.DeviceBuffer(n)
         _hip._ok(_hip.rt().hipMemset(src.ptr, 1, n), "hipMemset")
         _hip._ok(_hip.rt().hipMemcpy(dst.ptr, src.ptr, n, _hip.D2D), "hipMemcpy")
         _hip.synchronize()
-        log("[bench] traffic probe done: 2 config-4 forwards, 1 copy of 268435456 B")
+        log(f"[bench] traffic probe done: 2 config-{args.probe_config} forwards, 1 copy of 268435456 B")
         return
 
     for _ in range(args.warmup):
@@ -257,7 +271,8 @@ def main():
 
         # Config 2: the isolated quantised projections Y = X W^T at the encoder's four shapes,
         # M in {8, 512, 32768}, four formats; X f16 resident on the device (lle_gemm_f16_async),
-        # device time per call from HIP events (median of 20). Roofline: the dense fp16 MFMA peak
+        # device time per call from HIP events (median of 20); for M = 8 also a back-to-back
+        # sequence over distinct weight copies (HBM streaming). Roofline: the dense fp16 MFMA peak
         # for FLOP/s, and for bytes the quantised W + X f16 + Y f32 read/written once.
         from llmembed import quant as q_
 
@@ -287,16 +302,39 @@ def main():
                     ms = float(np.median(ts))
                     flops = 2.0 * M_c * N_c * K_c
                     nbytes = float(wq.nbytes) + M_c * K_c * 2 + M_c * N_c * 4
-                    c2.append(dict(fmt=tname, K=K_c, N=N_c, M=M_c, us=1e3 * ms, tflops=flops / ms / 1e9,
-                                   mfma_frac=flops / ms / 1e9 / PEAK_F16_TFLOPS, gbs=nbytes / ms / 1e6,
-                                   hbm_frac=nbytes / ms / 1e6 / PEAK_HBM_GBS))
+                    r2 = dict(fmt=tname, K=K_c, N=N_c, M=M_c, us=1e3 * ms, tflops=flops / ms / 1e9,
+                              mfma_frac=flops / ms / 1e9 / PEAK_F16_TFLOPS, gbs=nbytes / ms / 1e6,
+                              hbm_frac=nbytes / ms / 1e6 / PEAK_HBM_GBS)
+                    if M_c == 8:
+                        # weight streaming from HBM: back-to-back calls over distinct copies of the
+                        # weight (>= 520 MB in all, past the 256 MB MALL), device time of the sequence
+                        n_cp = min(2048, -(-520 * 2 ** 20 // wq.nbytes))
+                        os.environ["LLE_NO_F16_COPY"] = "1"  # M = 8 streams the quantised planes only
+                        try:
+                            cps = [llmembed.Weight(t, wq, K_c, N_c) for _ in range(n_cp)]
+                        finally:
+                            del os.environ["LLE_NO_F16_COPY"]
+                        for Wc in cps[:64]:
+                            Wc.gemm_f16_async(xbuf.value, 8, ybuf.value, pbuf.value, stream.h.value)
+                        e0.record(stream)
+                        for Wc in cps:
+                            Wc.gemm_f16_async(xbuf.value, 8, ybuf.value, pbuf.value, stream.h.value)
+                        e1.record(stream)
+                        ms_seq = e0.elapsed_ms(e1) / n_cp
+                        for Wc in cps:
+                            Wc.close()
+                        r2.update(seq_copies=n_cp, seq_us=1e3 * ms_seq, seq_gbs=nbytes / ms_seq / 1e6,
+                                  seq_hbm_frac=nbytes / ms_seq / 1e6 / PEAK_HBM_GBS)
+                    c2.append(r2)
                 W.close()
         extras["config2"] = c2
         for r in c2:
             if r["fmt"] in ("Q8_0", "Q4_K"):
                 log(f"[bench] config 2 {r['fmt']:4s} K={r['K']:4d} N={r['N']:4d} M={r['M']:5d}: {r['us']:8.1f} us "
                     f"{r['tflops']:7.1f} TFLOP/s ({100 * r['mfma_frac']:4.1f}% MFMA) {r['gbs']:7.0f} GB/s "
-                    f"({100 * r['hbm_frac']:4.1f}% HBM)")
+                    f"({100 * r['hbm_frac']:4.1f}% HBM)"
+                    + (f"; back-to-back over {r['seq_copies']} weight copies {r['seq_us']:.2f} us "
+                       f"{r['seq_gbs']:.0f} GB/s ({100 * r['seq_hbm_frac']:.1f}% HBM)" if "seq_us" in r else ""))
         del xbuf, ybuf, pbuf
 
         # Text path (EmbedBatch over strings): native host tokeniser, then lle_embed_texts'
