@@ -239,6 +239,26 @@ def main():
             mm.set_timing(False)
             o_c = do.download((Bc, D), np.float32)
             assert np.all(np.isfinite(o_c)), f"config {cfg} {mix}: non-finite output"
+            # the same sequences back to back on the device (lle_embed_packed_async)
+            lens_c = mask_c.sum(axis=1).astype(np.int64)
+            packed_c = np.concatenate([ids_c[b, :lens_c[b]] for b in range(Bc)]).astype(np.int32)
+            off_c = np.concatenate([[0], np.cumsum(lens_c)]).astype(np.int32)
+            dpi, dpo, dpy = (_hip.DeviceBuffer.from_array(packed_c), _hip.DeviceBuffer.from_array(off_c),
+                             _hip.DeviceBuffer(Bc * D * 4))
+
+            def stp():
+                check(L_.lle_embed_packed_async(mm.h, dpi.ptr, dpo.ptr, Bc, int(packed_c.size), Lc, D, dpy.ptr,
+                                                stream.h))
+
+            stp()
+            _hip.synchronize()
+            assert np.array_equal(dpy.download((Bc, D), np.float32).view(np.uint32), o_c.view(np.uint32)), \
+                f"config {cfg}: packed device entry != padded"
+            t_p = time.perf_counter()
+            for _ in range(steps):
+                stp()
+            _hip.synchronize()
+            packed_s = (time.perf_counter() - t_p) / steps
             # host-pointer entry point: padding is packed away before the first kernel
             emb_c = llmembed.Embedder(mm)
             h_c = emb_c.embed_padded(ids_c, mask_c)
@@ -251,14 +271,15 @@ def main():
             ms = 1000.0 * (t_b - t_a) / steps
             r = dict(mix=mix, batch=int(Bc), seq_len=int(Lc), valid_tokens=int(mask_c.sum()),
                      emb_per_s=Bc * steps / (t_b - t_a), ms_per_step=ms,
+                     device_packed_emb_per_s=Bc / packed_s, device_packed_ms=1e3 * packed_s,
                      host_api_packed_emb_per_s=Bc / host_s, host_api_packed_ms=1e3 * host_s,
                      shares={k: round(v["total_ms"] / tot_ms, 4) for k, v in kt_c.items()})
             if "attention" in kt_c:
                 at = kt_c["attention"]
                 r["attention_share"] = at["total_ms"] / tot_ms
                 r["attention_algorithmic_gbs"] = at["bytes"] / (at["total_ms"] * 1e-3) / 1e9
-            log(f"[bench] config {cfg} {mix}: {r['emb_per_s']:.1f} emb/s, {ms:.3f} ms/step; host API (packed rows) "
-                f"{Bc / host_s:.1f} emb/s"
+            log(f"[bench] config {cfg} {mix}: {r['emb_per_s']:.1f} emb/s, {ms:.3f} ms/step; packed on device "
+                f"{Bc / packed_s:.1f} emb/s; host API (packed rows) {Bc / host_s:.1f} emb/s"
                 + (f", attention {100 * r['attention_share']:.1f}% of kernel time at {r['attention_algorithmic_gbs']:.0f} GB/s (Q,K,V,O bytes)"
                    if "attention_share" in r else ""))
             mm.close()

@@ -139,7 +139,16 @@ int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t*
 int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L,
                            float* hidden);
 
-/* Device-side status word of the last async forward: 0 ok, 1 = a token id was out of range. */
+/* Packed batch on device pointers: the B sequences back to back in d_ids (T tokens, every one
+ * valid: no padding is stored or computed), d_seq_off [B+1] int32 with d_seq_off[0] = 0 and
+ * d_seq_off[B] = T; L >= the longest sequence (<= context_length). Row b of d_out equals
+ * lle_embed of sequence b bit for bit. Enqueued on `stream`; an inconsistent offset table is
+ * made safe and reported by lle_model_status (bit 2). */
+int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t* d_seq_off, int32_t B, int32_t T,
+                               int32_t L, int32_t out_dim, float* d_out, void* stream);
+
+/* Device-side status word of async forwards since the last host-pointer call (bits OR-ed):
+ * 1 = a token id was out of range (clamped), 2 = a packed batch's offsets were inconsistent. */
 int32_t lle_model_status(lle_model* m, int32_t* status);
 
 /* Kernel timing: enable (1) / disable (0) and read per-kernel-class HIP-event totals. */

@@ -204,6 +204,51 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
   for (int j = tid; j < od; j += 256) out[(size_t)b * od + j] = vals[j];
 }
 
+// Tables of a packed batch given as B sequences back to back (T tokens, offsets in[0..B]).
+// The offsets are first made safe to index with (one thread: B is small): nondecreasing, within
+// [0, T], no sequence longer than L; any change sets status bit 2 and the results of that call
+// are not meaningful, but every later access stays inside the buffers.
+__global__ void pack_offsets_kernel(const int32_t* __restrict__ in, int B, int T, int L, int32_t* __restrict__ off,
+                                    int32_t* status) {
+  if (threadIdx.x != 0) return;
+  bool bad = in[0] != 0;
+  int prev = 0;
+  off[0] = 0;
+  for (int b = 0; b < B; b++) {
+    const int e = in[b + 1];
+    const int c = min(max(e, prev), min(T, prev + L));
+    bad |= c != e;
+    off[b + 1] = c;
+    prev = c;
+  }
+  if (bad || prev != T) atomicOr(status, 2);
+}
+
+// tokrow[t] = b * L + position of row t; mask[b][p] = p < length of sequence b. Block B gives
+// rows that no sequence covers (only after a bad offset table) an in-range placeholder.
+__global__ void pack_tables_kernel(const int32_t* __restrict__ off, int B, int T, int L, int32_t* __restrict__ tokrow,
+                                   int32_t* __restrict__ mask) {
+  const int b = blockIdx.x;
+  if (b == B) {
+    for (int t = off[B] + (int)threadIdx.x; t < T; t += blockDim.x) tokrow[t] = 0;
+    return;
+  }
+  const int o = off[b], n = off[b + 1] - o;
+  for (int p = threadIdx.x; p < L; p += blockDim.x) {
+    mask[(size_t)b * L + p] = p < n ? 1 : 0;
+    if (p < n) tokrow[o + p] = b * L + p;
+  }
+}
+
+hipError_t launch_pack_tables(const int32_t* in_off, int B, int T, int L, int32_t* off, int32_t* tokrow,
+                              int32_t* mask, int32_t* status, hipStream_t st) {
+  hipLaunchKernelGGL(pack_offsets_kernel, dim3(1), dim3(64), 0, st, in_off, B, T, L, off, status);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(pack_tables_kernel, dim3(B + 1), dim3(256), 0, st, off, B, T, L, tokrow, mask);
+  return hipGetLastError();
+}
+
 hipError_t launch_pool(const float* h, const int32_t* mask, const int32_t* seq_off, int B, int L, int D, int out_dim,
                        float* out, hipStream_t st) {
   if (L > POOL_MAXL || D > 1024 || D % 4) return hipErrorInvalidValue;

@@ -941,6 +941,27 @@ int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t*
   return LLE_OK;
 }
 
+int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t* d_seq_off, int32_t B, int32_t T,
+                               int32_t L, int32_t out_dim, float* d_out, void* stream) {
+  int rc = check_batch(m, B, L);
+  if (rc) return rc;
+  if (!d_ids || !d_seq_off || !d_out) return fail(LLE_EINVAL, "null device pointer");
+  if (T < 1 || (int64_t)T > (int64_t)B * L) return fail(LLE_EINVAL, "T must be in [1, B * L]");
+  if (out_dim < 1) out_dim = 1;
+  std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  if ((rc = ensure_ws(m, B, L, T))) return rc;
+  hipStream_t st = stream ? (hipStream_t)stream : m->stream;
+  LAUNCH(launch_pack_tables(d_seq_off, B, T, L, m->seq_off, m->tokrow, m->mask, m->status, st));
+  Packing pk{T, m->tokrow, m->seq_off};
+  if ((rc = run_forward(m, d_ids, m->mask, B, L, out_dim, d_out, st, &pk))) return rc;
+  if (m->timing) {
+    LLE_HIP(hipStreamSynchronize(st));
+    collect_timing(m);
+  }
+  return LLE_OK;
+}
+
 int32_t lle_model_status(lle_model* m, int32_t* status) {
   if (!m || !status) return fail(LLE_EINVAL, "null argument");
   std::lock_guard<std::mutex> lk(m->mu);

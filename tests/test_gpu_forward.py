@@ -259,3 +259,46 @@ def test_small_batch_schedule_bitexact(gpu, small_spec, qkv_std):
         assert np.array_equal(bits(small[0]), bits(big[0])), (L, mask.tolist())
         if mask.any():
             compare(small, o.embed_batch(ids[None, :], mask[None, :]), f"small batch L={L}")
+
+
+def test_packed_device_entry(gpu, small_spec):
+    """lle_embed_packed_async: sequences back to back on the device (no padding stored or
+    computed) give the rows of the padded host entry bit for bit; an inconsistent offset table is
+    made safe and reported in the status word (bit 2)."""
+    import ctypes as C
+
+    from llmembed import _hip
+    from llmembed._lib import check, lib
+
+    e, o = models(small_spec, "Q8_0")
+    m = e.model()
+    D, V = small_spec.d_model, small_spec.vocab
+    rng = np.random.default_rng(77)
+    for lens in ([8], [1, 5, 16], [100, 3, 64, 1, 77], [300] * 6):
+        B, L = len(lens), max(lens)
+        seqs = [rng.integers(0, V, n).astype(np.int32) for n in lens]
+        ids = np.zeros((B, L), np.int32)
+        mask = np.zeros((B, L), np.int32)
+        for b, sq in enumerate(seqs):
+            ids[b, :sq.size], mask[b, :sq.size] = sq, 1
+        ref = e.embed_padded(ids, mask)
+        packed = np.concatenate(seqs)
+        off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        print(f"packed device entry: lens={lens}", flush=True)
+        di, do_, dy = _hip.DeviceBuffer.from_array(packed), _hip.DeviceBuffer.from_array(off), _hip.DeviceBuffer(B * D * 4)
+        check(lib().lle_embed_packed_async(m.h, di.ptr, do_.ptr, B, int(packed.size), L, D, dy.ptr, None))
+        _hip.synchronize()
+        assert np.array_equal(bits(dy.download((B, D), np.float32)), bits(ref)), lens
+        st = C.c_int32(-1)
+        check(lib().lle_model_status(m.h, C.byref(st)))
+        assert st.value == 0
+    # offsets that decrease and overrun T: clamped on the device, flagged, no fault
+    packed = rng.integers(0, V, 9).astype(np.int32)
+    di, do_, dy = (_hip.DeviceBuffer.from_array(packed), _hip.DeviceBuffer.from_array(np.array([0, 5, 3, 12], np.int32)),
+                   _hip.DeviceBuffer(3 * D * 4))
+    e.embed_padded(packed[None, :], np.ones((1, 9), np.int32))  # a host call clears the status word
+    check(lib().lle_embed_packed_async(m.h, di.ptr, do_.ptr, 3, 9, 9, D, dy.ptr, None))
+    _hip.synchronize()
+    st = C.c_int32(-1)
+    check(lib().lle_model_status(m.h, C.byref(st)))
+    assert st.value & 2
