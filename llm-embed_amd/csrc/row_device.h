@@ -33,15 +33,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // var = sumSq/n - mean^2, invStd = float32(1/sqrt(float64(var + eps))),
 // y = (x - mean) * invStd * w + b. One wave per row; element j = lane + 64 i.
 // LayerNorm of one row held as x[i] = element lane + 64 i; x is replaced by the output y.
-__device__ __forceinline__ void ln_apply(float* x, int ne, int D, const float* w, const float* b, float eps,
-                                         int lane) {
-  float wv[MAXE], bv[MAXE];  // issued before the reductions so their latency overlaps them
-#pragma unroll
-  for (int i = 0; i < MAXE; i++)
-    if (i < ne) {
-      wv[i] = w[lane + 64 * i];
-      bv[i] = b[lane + 64 * i];
-    }
+// ln_apply with the row's weights and biases already in registers (wv[i], bv[i] for element
+// lane + 64 i): callers load them before the row itself, so their latency overlaps the row's.
+__device__ __forceinline__ void ln_apply_wb(float* x, int ne, int D, const float* wv, const float* bv, float eps) {
   float s = 0.f, ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXE; i++)
@@ -58,6 +52,18 @@ __device__ __forceinline__ void ln_apply(float* x, int ne, int D, const float* w
 #pragma unroll
   for (int i = 0; i < MAXE; i++)
     if (i < ne) x[i] = (x[i] - mean) * inv * wv[i] + bv[i];
+}
+
+__device__ __forceinline__ void ln_apply(float* x, int ne, int D, const float* w, const float* b, float eps,
+                                         int lane) {
+  float wv[MAXE], bv[MAXE];  // issued before the reductions so their latency overlaps them
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) {
+      wv[i] = w[lane + 64 * i];
+      bv[i] = b[lane + 64 * i];
+    }
+  ln_apply_wb(x, ne, D, wv, bv, eps);
 }
 
 // LayerNormInPlace of one row into hrow (f32) and h16row (f16).

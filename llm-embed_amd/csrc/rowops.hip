@@ -8,29 +8,61 @@ namespace lle {
 
 // Embedding stage (internal/embed/bert.go:220-249, getEmbedding :290-316):
 // h = deq(token_embd[id]) + deq(token_types[0]), then LayerNorm(token_embd_norm).
+// One wave per token. The wave first issues the loads that do not depend on the token id (the
+// type row and the LayerNorm weights), then copies the token's GGUF row into LDS with whole
+// 16-byte (or 2-byte, for rows of odd 8-byte length) loads, and dequantises from there: the
+// per-element scale and code loads of a raw row would otherwise be a dependent global round
+// trip each.
 template <int TY>
 __global__ __launch_bounds__(256) void embed_ln_kernel(EmbedArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= a.T) return;
+  constexpr int RB = 4 * 64 * MAXE;  // bytes of the widest row on the path (F32 at the largest d_model)
+  __shared__ __attribute__((aligned(16))) uint8_t srow[4][RB];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wv;
+  if (t >= a.T) return;  // wave-uniform; the LDS row below is this wave's alone
+  const int ne = a.D / 64;
+  float ty[MAXE], lw[MAXE], lb[MAXE];
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) {
+      const int j = lane + 64 * i;
+      ty[i] = a.type0[j];
+      lw[i] = a.w[j];
+      lb[i] = a.b[j];
+    }
   int id = a.ids[t];
   if (id < 0 || id >= a.vocab) {
     if (lane == 0) atomicOr(a.status, 1);
     id = 0;
   }
   const uint8_t* row = a.tok + (size_t)id * a.tok_row_bytes;
-  const int ne = a.D / 64;
+  const int nb = (int)a.tok_row_bytes;
+  if ((nb & 15) == 0 && (((uintptr_t)row) & 15) == 0) {
+    for (int o = lane * 16; o < nb; o += 64 * 16) *(uint4*)&srow[wv][o] = *(const uint4*)(row + o);
+  } else {
+    for (int o = lane * 2; o < nb; o += 64 * 2) *(uint16_t*)&srow[wv][o] = *(const uint16_t*)(row + o);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float x[MAXE];
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) x[i] = deq_raw_t<TY>(srow[wv], lane + 64 * i) + ty[i];
+  ln_apply_wb(x, ne, a.D, lw, lb, a.eps);
+  float* hrow = a.h + (size_t)t * a.D;
+  __half* h16row = a.h16 + (size_t)t * a.D;
 #pragma unroll
   for (int i = 0; i < MAXE; i++)
     if (i < ne) {
       const int j = lane + 64 * i;
-      x[i] = deq_raw_t<TY>(row, j) + a.type0[j];
+      hrow[j] = x[i];
+      h16row[j] = __float2half_rn(x[i]);
     }
-  ln_row(x, ne, a.D, a.w, a.b, a.eps, lane, a.h + (size_t)t * a.D, a.h16 + (size_t)t * a.D);
 }
 
 hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st) {
+  if (a.tok_row_bytes > 4 * 64 * MAXE || a.tok_row_bytes % 2 || a.D > 64 * MAXE) return hipErrorInvalidValue;
   const dim3 g((a.T + 3) / 4), blk(256);
   switch (a.tok_type) {  // one instantiation per format keeps every row load in one basic block
     case 0: hipLaunchKernelGGL(embed_ln_kernel<0>, g, blk, 0, st, a); break;
