@@ -57,6 +57,43 @@ def test_config1_full_model(gpu, full_spec):
     compare(e.embed(ids[0]), o.embed(ids[0]), "c1")
 
 
+def test_config4_full_size_properties(gpu, full_spec):
+    """Config 4 at its full size (full 12-layer Q8_0 model, B=256, L=128: the 32768-token
+    schedule of the benchmark). Size-independent properties: finite unit-norm rows; a second run
+    gives the same bits; rows equal the same sequences embedded alone (the <= 64-token schedule:
+    split-K small GEMMs, fused LayerNorm prologues, 64-query attention) bit for bit; and two rows
+    match the oracle."""
+    e, o = models(full_spec, "Q8_0", synth.CONFIG_SEED + 4)
+    ids, mask = synth.config_inputs(4)
+    assert ids.shape == (256, 128) and int(mask.sum()) == 256 * 128
+    batch = e.embed_padded(ids, mask)
+    assert batch.shape == (256, full_spec.d_model) and np.all(np.isfinite(batch))
+    norms = np.linalg.norm(batch.astype(np.float64), axis=1)
+    assert np.abs(norms - 1.0).max() < 1e-5, np.abs(norms - 1.0).max()
+    assert np.array_equal(bits(e.embed_padded(ids, mask)), bits(batch))
+    for i in (0, 77, 255):
+        assert np.array_equal(bits(e.embed(ids[i])), bits(batch[i])), i
+    compare(batch[[0, 200]], np.stack([o.embed(ids[0]), o.embed(ids[200])]), "c4 full size")
+
+
+def test_config5_full_size_properties(gpu, full_spec):
+    """Config 5 at its full size (full 12-layer Q8_0 model, B=8, lengths in [1024, 2048] padded
+    to 2048): finite unit-norm rows, rows equal each sequence embedded alone bit for bit, the
+    shortest sequence matches the oracle."""
+    e, o = models(full_spec, "Q8_0", synth.CONFIG_SEED + 5)
+    ids, mask = synth.config_inputs(5)
+    B, L = ids.shape
+    lens = mask.sum(axis=1)
+    assert (B, L) == (8, 2048) and lens.min() >= 1024
+    batch = e.embed_padded(ids, mask)
+    assert np.all(np.isfinite(batch))
+    assert np.abs(np.linalg.norm(batch.astype(np.float64), axis=1) - 1.0).max() < 1e-5
+    i0 = int(np.argmin(lens))
+    for i in sorted({i0, int(np.argmax(lens))}):
+        assert np.array_equal(bits(e.embed(ids[i, :lens[i]])), bits(batch[i])), i
+    compare(batch[i0], o.embed(ids[i0, :lens[i0]]), "c5 full size")
+
+
 def test_hidden_states(gpu, small_spec):
     e, o = models(small_spec, "Q8_0")
     ids = np.random.default_rng(3).integers(0, small_spec.vocab, 33).astype(np.int32)
