@@ -1122,6 +1122,36 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
       }
     }
   };
+  // LayerNorm prologue: wave w normalises rows w, w + 4 (and w + 8, w + 12). The inputs of rows
+  // 0..7 (all rows of a batch of <= 8 tokens) and the LayerNorm weights are loaded before the
+  // weight stream: vector loads complete in issue order, so issued after it they could not be
+  // used before the whole stream had arrived, and the LayerNorm would only start then.
+  constexpr int NPART = LNP > 0 ? LNP - 1 : 0, NE = LNP > 0 ? KF / 64 : 1;
+  constexpr int LE = LNP > 0 ? MAXE : 1, LP = NPART > 0 ? NPART : 1;
+  float lw[LE], lb[LE], lx[2][LE], lpv[2][LE][LP];
+  auto ln_load = [&](int r0, float (&x)[2][LE], float (&pv)[2][LE][LP]) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int r = r0 + wave + 4 * h;
+      if (r < M) {
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+          const int j = lane + 64 * i;
+          x[h][i] = p.ln.src[(size_t)r * KF + j];
+#pragma unroll
+          for (int q = 0; q < NPART; q++) pv[h][i][q] = p.ln.part[((size_t)q * M + r) * KF + j];
+        }
+      }
+    }
+  };
+  if constexpr (LNP > 0) {
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+      lw[i] = p.ln.w[lane + 64 * i];
+      lb[i] = p.ln.b[lane + 64 * i];
+    }
+    ln_load(0, lx, lpv);
+  }
   if constexpr (AHEAD) {
 #pragma unroll
     for (int pc = 0; pc < NPIECE; pc++) load_piece(pc, kbase + pc * PK);
@@ -1129,25 +1159,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
 
   if constexpr (LNP > 0) {
     static_assert(BM == 16 && DIRECT && KF <= 64 * MAXE && NT == 256, "LayerNorm prologue shape");
-    constexpr int NPART = LNP - 1, NE = KF / 64;
-    // wave w normalises rows w, w + 4 (and w + 8, w + 12): each pair's loads are issued together
-#pragma unroll
-    for (int r0 = 0; r0 < BM; r0 += 8) {
-      float x[2][MAXE];
-      float pv[2][MAXE][NPART > 0 ? NPART : 1];
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int r = r0 + wave + 4 * h;
-        if (r < M) {
-#pragma unroll
-          for (int i = 0; i < NE; i++) {
-            const int j = lane + 64 * i;
-            x[h][i] = p.ln.src[(size_t)r * KF + j];
-#pragma unroll
-            for (int q = 0; q < NPART; q++) pv[h][i][q] = p.ln.part[((size_t)q * M + r) * KF + j];
-          }
-        }
-      }
+    auto ln_rows = [&](int r0, float (&x)[2][LE], float (&pv)[2][LE][LP]) {
 #pragma unroll
       for (int h = 0; h < 2; h++) {
         const int r = r0 + wave + 4 * h;
@@ -1161,7 +1173,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
               x[h][i] = x[h][i] + t;
             }
           }
-          ln_apply(x[h], NE, KF, p.ln.w, p.ln.b, p.ln.eps, lane);
+          ln_apply_wb(x[h], NE, KF, lw, lb, p.ln.eps);
           if (blockIdx.x == 0 && blockIdx.y == 0) {
 #pragma unroll
             for (int i = 0; i < NE; i++) p.ln.out[(size_t)r * KF + lane + 64 * i] = x[h][i];
@@ -1176,7 +1188,11 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
           sXf[r][(((k >> 3) ^ (r & 7)) << 3) + (k & 7)] = (_Float16)__float2half_rn(x[h][i]);
         }
       }
-    }
+    };
+    ln_rows(0, lx, lpv);
+    float x8[2][LE], pv8[2][LE][LP];
+    ln_load(8, x8, pv8);  // rows 8..15 (no loads when M <= 8)
+    ln_rows(8, x8, pv8);
   }
 
   const int lr = lane & 15, lg = lane >> 4;
