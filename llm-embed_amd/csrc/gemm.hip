@@ -1094,8 +1094,12 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
   constexpr bool AHEAD = FMT != 0;  // f32 weights are too wide to hold every piece in registers
   constexpr int NP = AHEAD ? NPIECE : 1;
   constexpr int KF = NPIECE * PK;  // LNP: the whole K
-  __shared__ __attribute__((aligned(16))) _Float16 sW[BN][LDW];
-  __shared__ __attribute__((aligned(16))) _Float16 sX[LNP ? 1 : BM][LDW];
+  // 16-row blocks (the smallest batches, latency-bound) decode every piece into its own LDS
+  // buffer behind one barrier, and the MFMA chain then runs over the whole chunk without stops
+  constexpr bool ALLW = AHEAD && BM == 16;
+  constexpr int NWB = ALLW ? NPIECE : 1;
+  __shared__ __attribute__((aligned(16))) _Float16 sW[NWB][BN][LDW];
+  __shared__ __attribute__((aligned(16))) _Float16 sX[LNP ? 1 : NWB][LNP ? 1 : BM][LDW];
   __shared__ __attribute__((aligned(16))) _Float16 sXf[LNP ? BM : 1][LNP ? KF : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1205,17 +1209,32 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
   floatx4 acc[TB];
 #pragma unroll
   for (int j = 0; j < TB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto mma_piece = [&](int pc, int ws) {
+#pragma unroll
+    for (int ks = 0; ks < PK / 32; ks++) {
+      const half8 af = *(const half8*)&sW[ws][wave * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+#pragma unroll
+      for (int j = 0; j < TB; j++) {
+        half8 bf;
+        if constexpr (LNP > 0)
+          bf = *(const half8*)&sXf[j * 16 + lr][(pc * (PK / 8) + swz(lr, ks * 4 + lg)) * 8];
+        else
+          bf = *(const half8*)&sX[ws][j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
+        acc[j] = mfma16(af, bf, acc[j]);
+      }
+    }
+  };
 #pragma unroll
   for (int pc = 0; pc < NPIECE; pc++) {
-    const int slot = AHEAD ? pc : 0;
+    const int slot = AHEAD ? pc : 0, ws = ALLW ? pc : 0;
     const int kb = kbase + pc * PK;
     if constexpr (!AHEAD) load_piece(0, kb);
-    if (pc > 0) __syncthreads();
+    if (!ALLW && pc > 0) __syncthreads();
     if constexpr (LNP == 0) {
 #pragma unroll
       for (int i = 0; i < XPT; i++) {
         const int cc = tid + i * NT;
-        if (cc < XCH) *(uint4*)&sX[cc >> 5][swz(cc >> 5, cc & 31) * 8] = xr[slot][i];
+        if (cc < XCH) *(uint4*)&sX[ws][cc >> 5][swz(cc >> 5, cc & 31) * 8] = xr[slot][i];
       }
     }
 #pragma unroll
@@ -1223,23 +1242,18 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
       const int u = tid + i * NT, row = u >> 4, sg = u & 15;
       uint4 lo, hi;
       decode_seg_h<FMT>(wr[slot][i], kb + sg * 16, lo, hi);
-      *(uint4*)&sW[row][swz(row, 2 * sg) * 8] = lo;
-      *(uint4*)&sW[row][swz(row, 2 * sg + 1) * 8] = hi;
+      *(uint4*)&sW[ws][row][swz(row, 2 * sg) * 8] = lo;
+      *(uint4*)&sW[ws][row][swz(row, 2 * sg + 1) * 8] = hi;
     }
+    if constexpr (!ALLW) {
+      __syncthreads();
+      mma_piece(pc, 0);
+    }
+  }
+  if constexpr (ALLW) {
     __syncthreads();
 #pragma unroll
-    for (int ks = 0; ks < PK / 32; ks++) {
-      const half8 af = *(const half8*)&sW[wave * 16 + lr][swz(lr, ks * 4 + lg) * 8];
-#pragma unroll
-      for (int j = 0; j < TB; j++) {
-        half8 bf;
-        if constexpr (LNP > 0)
-          bf = *(const half8*)&sXf[j * 16 + lr][(pc * (PK / 8) + swz(lr, ks * 4 + lg)) * 8];
-        else
-          bf = *(const half8*)&sX[j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
-        acc[j] = mfma16(af, bf, acc[j]);
-      }
-    }
+    for (int pc = 0; pc < NPIECE; pc++) mma_piece(pc, pc);
   }
   if constexpr (DIRECT) {
     // single-chunk K: the total is 0 + this chunk, finished here with the epilogue
