@@ -36,7 +36,7 @@ __device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const 
 
 // NW waves per block (16 queries each). K / V^T tiles are double-buffered: the global loads of
 // key tile kt+1 are issued before tile kt's MFMAs and land in the other LDS buffer afterwards.
-template <int NW>
+template <int NW, bool EARLY>
 __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
   constexpr int NT = NW * 64, AQB = NW * 16;
   constexpr int CPT = (AK * HD / 8) / NT;  // 16-byte chunks of each tile per thread
@@ -70,15 +70,55 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
       qf[ks] = half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
+  uint4 kreg[CPT], vreg[CPT];
+  int mreg = 0;
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+      const int c = tid + i * NT, row = c >> 3, ch = c & 7;
+      const int key = kt * AK + row;
+      kreg[i] = key < Lk ? *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8) : uint4{0, 0, 0, 0};
+      const int k0 = kt * AK + ch * 8;
+      uint4 vv = uint4{0, 0, 0, 0};
+      if (k0 < Lk) {
+        vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
+        if (k0 + 8 > Lk) {  // zero the keys at and past Lk (columns never written)
+          const int nv = Lk - k0;
+          vv.x &= (nv > 0 ? 0xFFFFu : 0u) | (nv > 1 ? 0xFFFF0000u : 0u);
+          vv.y &= (nv > 2 ? 0xFFFFu : 0u) | (nv > 3 ? 0xFFFF0000u : 0u);
+          vv.z &= (nv > 4 ? 0xFFFFu : 0u) | (nv > 5 ? 0xFFFF0000u : 0u);
+          vv.w &= (nv > 6 ? 0xFFFFu : 0u) | (nv > 7 ? 0xFFFF0000u : 0u);
+        }
+      }
+      vreg[i] = vv;
+    }
+    if (tid < AK) {
+      const int key = kt * AK + tid;
+      mreg = key < L ? a.mask[(size_t)b * L + key] : 0;
+    }
+  };
   // [klo, khi): from the first to one past the last valid key of the sequence (all L keys when
-  // none is valid: the softmax is then uniform over every key)
+  // none is valid: the softmax is then uniform over every key). EARLY (launched when one load
+  // per thread covers the mask row, L <= NT): key tile 0's loads are issued right after the
+  // mask load, before the scan needs them (the first valid key is nearly always in tile 0;
+  // otherwise the tile is loaded again below). With longer rows they would sit in front of the
+  // scan's remaining mask loads (loads complete in issue order).
   __shared__ int sLo[NW], sHi[NW];
   int klo, khi;
   {
     const int32_t* mrow = a.mask + (size_t)b * L;
-    int lo = L, hi = -1;
+    int lo = L, hi = -1, i0 = tid;
+    if constexpr (EARLY) {
+      const int mv0 = tid < L ? mrow[tid] : 0;
+      gload(0);
+      if (mv0 != 0) {
+        lo = tid;
+        hi = tid;
+      }
+      i0 = tid + NT;
+    }
 #pragma unroll 4
-    for (int i = tid; i < L; i += NT) {
+    for (int i = i0; i < L; i += NT) {
       if (mrow[i] != 0) {
         lo = min(lo, i);
         hi = max(hi, i);
@@ -120,33 +160,6 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
   float m_run = -INFINITY, lsum = 0.f, smin = INFINITY;
   floatx4 o[4];
 
-  uint4 kreg[CPT], vreg[CPT];
-  int mreg = 0;
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < CPT; i++) {
-      const int c = tid + i * NT, row = c >> 3, ch = c & 7;
-      const int key = kt * AK + row;
-      kreg[i] = key < Lk ? *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8) : uint4{0, 0, 0, 0};
-      const int k0 = kt * AK + ch * 8;
-      uint4 vv = uint4{0, 0, 0, 0};
-      if (k0 < Lk) {
-        vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
-        if (k0 + 8 > Lk) {  // zero the keys at and past Lk (columns never written)
-          const int nv = Lk - k0;
-          vv.x &= (nv > 0 ? 0xFFFFu : 0u) | (nv > 1 ? 0xFFFF0000u : 0u);
-          vv.y &= (nv > 2 ? 0xFFFFu : 0u) | (nv > 3 ? 0xFFFF0000u : 0u);
-          vv.z &= (nv > 4 ? 0xFFFFu : 0u) | (nv > 5 ? 0xFFFF0000u : 0u);
-          vv.w &= (nv > 6 ? 0xFFFFu : 0u) | (nv > 7 ? 0xFFFF0000u : 0u);
-        }
-      }
-      vreg[i] = vv;
-    }
-    if (tid < AK) {
-      const int key = kt * AK + tid;
-      mreg = key < L ? a.mask[(size_t)b * L + key] : 0;
-    }
-  };
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
@@ -175,7 +188,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
     const float m_fix = m_run;
 
     __syncthreads();  // the buffers of a previous pass are no longer read
-    gload(t0);
+    if (!EARLY || fixed || t0 != 0) gload(t0);  // else tile 0 is already in registers
     sstore(0);
     __syncthreads();
     for (int kt = t0; kt < t1; kt++) {
@@ -283,10 +296,13 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   // 128-query blocks read each key tile once per 128 queries; short sequences keep 64
   if (a.L > 64) {
     const dim3 grid((a.L + 127) / 128, a.H, a.B);
-    hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(512), 0, st, a);
+    if (a.L <= 512)
+      hipLaunchKernelGGL((attention_kernel<8, true>), grid, dim3(512), 0, st, a);
+    else
+      hipLaunchKernelGGL((attention_kernel<8, false>), grid, dim3(512), 0, st, a);
   } else {
     const dim3 grid(1, a.H, a.B);
-    hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attention_kernel<4, true>), grid, dim3(256), 0, st, a);
   }
   return hipGetLastError();
 }
