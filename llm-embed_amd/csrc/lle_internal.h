@@ -145,6 +145,12 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 
 hipError_t launch_pool(const float* h, const int32_t* mask, const int32_t* seq_off, int B, int L, int D, int out_dim,
                        float* out, hipStream_t st);
+// launch_reduce_resid_ln (rows of N = D, nch = 4) followed by launch_pool, in one kernel that
+// keeps the LayerNorm rows in LDS; bit-identical to the two kernels. The LayerNorm rows are not
+// stored.
+hipError_t launch_reduce_ln_pool(const float* part, int nch, int M, const float* src, const float* w, const float* b,
+                                 float eps, const int32_t* mask, const int32_t* seq_off, int B, int L, int D,
+                                 int out_dim, float* out, hipStream_t st);
 // packed batch tables from caller offsets in_off[B+1]: sanitised offsets, tokrow [T], mask [B][L]
 hipError_t launch_pack_tables(const int32_t* in_off, int B, int T, int L, int32_t* off, int32_t* tokrow,
                               int32_t* mask, int32_t* status, hipStream_t st);

@@ -151,15 +151,11 @@ hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, cons
 // is accumulated in f64. One block per sequence: the kept rows are first compacted (in order)
 // into an LDS list, then each thread sums 4 adjacent columns with 16 row loads in flight.
 constexpr int POOL_MAXL = 8192;
-__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ mask,
-                                                   const int32_t* __restrict__ seq_off, int L, int D, int out_dim,
-                                                   float* __restrict__ out) {
-  const int b = blockIdx.x, tid = threadIdx.x;
-  __shared__ double red[256];
-  __shared__ __align__(16) float vals[1024];
-  __shared__ int rows[POOL_MAXL];
-  __shared__ int wcount[5];
-  // ordered compaction of kept rows: per-wave ballot + prefix over the 4 waves
+
+// Ordered compaction of sequence b's kept positions (mask == 1) into rows[]: per-wave ballot +
+// prefix over the 4 waves of a 256-thread block. Returns their count.
+__device__ int pool_compact(const int32_t* __restrict__ mask, int b, int L, int* rows, int* wcount) {
+  const int tid = threadIdx.x;
   int base = 0;
   for (int i0 = 0; i0 < L; i0 += 256) {
     const int i = i0 + tid;
@@ -174,7 +170,46 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
     base += wcount[0] + wcount[1] + wcount[2] + wcount[3];
     __syncthreads();
   }
-  const int count = base;
+  return base;
+}
+
+// L2Normalize of the pooled row vals[0..D) over the first n values, twice when truncating
+// (embedder.go:65-68), then min(out_dim, D) values to out.
+__device__ void pool_finish(float* vals, double* red, int D, int out_dim, float* __restrict__ out) {
+  const int tid = threadIdx.x;
+  int n = D;
+  for (int pass = 0; pass < 2; pass++) {
+    double acc = 0.0;
+    for (int j = tid; j < n; j += 256) acc += (double)vals[j] * (double)vals[j];
+    red[tid] = acc;
+    __syncthreads();
+    for (int s2 = 128; s2 > 0; s2 >>= 1) {
+      if (tid < s2) red[tid] += red[tid + s2];
+      __syncthreads();
+    }
+    const double norm = sqrt(red[0]);
+    __syncthreads();
+    if (norm != 0.0) {
+      const float inv = (float)(1.0 / norm);
+      for (int j = tid; j < n; j += 256) vals[j] = vals[j] * inv;
+    }
+    __syncthreads();
+    if (out_dim >= D) break;
+    n = out_dim;
+  }
+  const int od = out_dim < D ? out_dim : D;
+  for (int j = tid; j < od; j += 256) out[j] = vals[j];
+}
+
+__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ mask,
+                                                   const int32_t* __restrict__ seq_off, int L, int D, int out_dim,
+                                                   float* __restrict__ out) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  __shared__ double red[256];
+  __shared__ __align__(16) float vals[1024];
+  __shared__ int rows[POOL_MAXL];
+  __shared__ int wcount[5];
+  const int count = pool_compact(mask, b, L, rows, wcount);
   // packed rows: sequence b starts at row seq_off[b] and its kept positions all lie before
   // seq_off[b + 1] - seq_off[b] (positions past its last valid token were dropped)
   const float* hb = h + (size_t)(seq_off ? seq_off[b] : b * L) * D;
@@ -211,29 +246,94 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
     *(float4*)(vals + c0) = s;
   }
   __syncthreads();
-  // L2Normalize over the first n values, twice when truncating (embedder.go:65-68)
-  int n = D;
-  for (int pass = 0; pass < 2; pass++) {
-    double acc = 0.0;
-    for (int j = tid; j < n; j += 256) acc += (double)vals[j] * (double)vals[j];
-    red[tid] = acc;
-    __syncthreads();
-    for (int s2 = 128; s2 > 0; s2 >>= 1) {
-      if (tid < s2) red[tid] += red[tid + s2];
-      __syncthreads();
+  pool_finish(vals, red, D, out_dim, out + (size_t)b * (out_dim < D ? out_dim : D));
+}
+
+// The last LayerNorm of a small forward fused with MeanPool + L2Normalize, one block per
+// sequence. Its kept rows are normalised 16 at a time into LDS with reduce_resid_ln_kernel's
+// arithmetic (residual + (0 + chunk partials in order), ln_row's LayerNorm), and added in row
+// order as pool_kernel adds them; the scaling, norm and Matryoshka tail are pool_kernel's. So
+// the output equals reduce_resid_ln_kernel followed by pool_kernel bit for bit, without the
+// LayerNorm rows going through global memory.
+constexpr int RLP_ROWS = 16;
+template <int NCH>
+__global__ __launch_bounds__(256) void reduce_ln_pool_kernel(const float* __restrict__ part, int M, const float* src,
+                                                             const float* w, const float* bb, float eps,
+                                                             const int32_t* __restrict__ mask,
+                                                             const int32_t* __restrict__ seq_off, int L, int D,
+                                                             int out_dim, float* __restrict__ out) {
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  __shared__ double red[256];
+  __shared__ __align__(16) float vals[1024];
+  __shared__ int rows[POOL_MAXL];
+  __shared__ int wcount[5];
+  __shared__ __align__(16) float lnrow[RLP_ROWS][1024];
+  const int count = pool_compact(mask, b, L, rows, wcount);
+  const int row0 = seq_off ? seq_off[b] : b * L;
+  const int ne = D / 64, c0 = 4 * tid;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i0 = 0; i0 < count; i0 += RLP_ROWS) {
+    for (int k = wv; k < RLP_ROWS; k += 4) {  // wave wv: rows i0 + wv, + 4, + 8, + 12
+      if (i0 + k < count) {
+        const int t = row0 + rows[i0 + k];
+        const float* srow = src + (size_t)t * D;
+        float pv[MAXE][NCH], x[MAXE];
+#pragma unroll
+        for (int i = 0; i < MAXE; i++)
+          if (i < ne) {
+            const int j = lane + 64 * i;
+            x[i] = srow[j];
+#pragma unroll
+            for (int c = 0; c < NCH; c++) pv[i][c] = part[((size_t)c * M + t) * D + j];
+          }
+#pragma unroll
+        for (int i = 0; i < MAXE; i++)
+          if (i < ne) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCH; c++) acc += pv[i][c];
+            x[i] = x[i] + acc;
+          }
+        ln_apply(x, ne, D, w, bb, eps, lane);
+#pragma unroll
+        for (int i = 0; i < MAXE; i++)
+          if (i < ne) lnrow[k][lane + 64 * i] = x[i];
+      }
     }
-    const double norm = sqrt(red[0]);
     __syncthreads();
-    if (norm != 0.0) {
-      const float inv = (float)(1.0 / norm);
-      for (int j = tid; j < n; j += 256) vals[j] = vals[j] * inv;
+    if (c0 < D) {
+      const int nr = count - i0 < RLP_ROWS ? count - i0 : RLP_ROWS;
+      for (int u = 0; u < nr; u++) {
+        const float4 v = *(const float4*)&lnrow[u][c0];
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      }
     }
     __syncthreads();
-    if (out_dim >= D) break;
-    n = out_dim;
   }
-  const int od = out_dim < D ? out_dim : D;
-  for (int j = tid; j < od; j += 256) out[(size_t)b * od + j] = vals[j];
+  if (c0 < D) {
+    if (count != 0) {
+      const float inv = 1.0f / (float)count;
+      s.x *= inv;
+      s.y *= inv;
+      s.z *= inv;
+      s.w *= inv;
+    }
+    *(float4*)(vals + c0) = s;
+  }
+  __syncthreads();
+  pool_finish(vals, red, D, out_dim, out + (size_t)b * (out_dim < D ? out_dim : D));
+}
+
+hipError_t launch_reduce_ln_pool(const float* part, int nch, int M, const float* src, const float* w, const float* b,
+                                 float eps, const int32_t* mask, const int32_t* seq_off, int B, int L, int D,
+                                 int out_dim, float* out, hipStream_t st) {
+  if (L > POOL_MAXL || D > 1024 || D % 64 || nch != 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(reduce_ln_pool_kernel<4>, dim3(B), dim3(256), 0, st, part, M, src, w, b, eps, mask, seq_off, L,
+                     D, out_dim, out);
+  return hipGetLastError();
 }
 
 // Tables of a packed batch given as B sequences back to back (T tokens, offsets in[0..B]).

@@ -334,14 +334,14 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
         LAUNCH(launch_gemm_partials(g, st));
       }
     }
-    {
-      const Layer& last = m->layers[m->n_layer - 1];
+    const Layer& last = m->layers[m->n_layer - 1];
+    if (d_out) {  // the last LayerNorm's rows only feed the pool: one kernel, rows kept in LDS
+      Scope s(m, st, "pool", 0, (double)T * D * 24);
+      LAUNCH(launch_reduce_ln_pool(m->part, 4, T, m->h2, last.onw, last.onb, m->eps, d_mask, seq_off, B, L, D,
+                                   out_dim, d_out, st));
+    } else {
       Scope s(m, st, "ln", 0, (double)T * D * 26);
       LAUNCH(launch_reduce_resid_ln(m->part, 4, T, D, m->h2, m->h, m->h16, last.onw, last.onb, m->eps, st));
-    }
-    if (d_out) {
-      Scope s(m, st, "pool", 0, (double)T * D * 4);
-      LAUNCH(launch_pool(m->h, d_mask, seq_off, B, L, D, out_dim, d_out, st));
     }
     return LLE_OK;
   }
