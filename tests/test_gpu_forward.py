@@ -186,6 +186,52 @@ def test_matryoshka(gpu, small_spec):
         compare(v, o.embed(ids, out_dim=d), f"matryoshka {d}")
 
 
+def test_small_forward_pool_paths(gpu, small_spec):
+    """Forwards of <= 16 tokens end in one kernel (last LayerNorm + mean-pool + L2, rows kept in
+    LDS). Mask holes, several packed sequences and Matryoshka widths through it must equal the
+    same rows inside a larger batch (separate LayerNorm and pool kernels) bit for bit, and
+    match the oracle."""
+    e, o = models(small_spec, "Q8_0")
+    rng = np.random.default_rng(17)
+    long_row = rng.integers(0, small_spec.vocab, 40).astype(np.int32)
+
+    def in_big_batch(ids, mask):  # the rows again, beside a 40-token sequence (> 16 tokens)
+        B, L = ids.shape
+        big_ids = np.zeros((B + 1, 40), np.int32)
+        big_mask = np.zeros((B + 1, 40), np.int32)
+        big_ids[:B, :L], big_mask[:B, :L] = ids, mask
+        big_ids[B], big_mask[B] = long_row, 1
+        return e.embed_padded(big_ids, big_mask)[:B]
+
+    # one sequence with mask holes (first, interior and last positions)
+    ids = rng.integers(0, small_spec.vocab, (1, 12)).astype(np.int32)
+    mask = np.ones((1, 12), np.int32)
+    mask[0, [0, 5, 11]] = 0
+    small = e.embed_padded(ids, mask)
+    assert np.array_equal(bits(small), bits(in_big_batch(ids, mask)))
+    compare(small[0], o.embed(ids[0], mask[0]), "small forward, mask holes")
+    # three sequences packed into 12 tokens, right-padded to 6
+    lens = [3, 5, 4]
+    ids = rng.integers(0, small_spec.vocab, (3, 6)).astype(np.int32)
+    mask = (np.arange(6)[None, :] < np.array(lens)[:, None]).astype(np.int32)
+    small = e.embed_padded(ids, mask)
+    assert np.array_equal(bits(small), bits(in_big_batch(ids, mask)))
+    for b, n in enumerate(lens):
+        compare(small[b], o.embed(ids[b, :n]), f"small forward, packed row {b}")
+    # Matryoshka widths
+    ids = rng.integers(0, small_spec.vocab, (1, 10)).astype(np.int32)
+    mask = np.ones((1, 10), np.int32)
+    for d in (256, 64):
+        e.set_target_dim(d)
+        try:
+            small = e.embed_padded(ids, mask)
+            big = in_big_batch(ids, mask)
+        finally:
+            e.set_target_dim(768)
+        assert small.shape == (1, d) and np.array_equal(bits(small), bits(big)), d
+        compare(small[0], o.embed(ids[0], out_dim=d), f"small forward, matryoshka {d}")
+
+
 def test_cutoff_active_attention(gpu, small_spec):
     """Large attention logits (qkv weights N(0, 0.3)): the softmax's x < -10 cutoff drops keys,
     exercising the kernel's fixed-max second pass."""
