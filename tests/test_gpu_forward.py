@@ -76,6 +76,24 @@ def test_config4_full_size_properties(gpu, full_spec):
     compare(batch[[0, 200]], np.stack([o.embed(ids[0]), o.embed(ids[200])]), "c4 full size")
 
 
+def test_config3_full_size_properties(gpu, full_spec):
+    """Config 3 at its full size (full 12-layer Q4_K_M model: Q4_K / Q6_K projections, B=64,
+    lengths in [16, 128] padded to 128): finite unit-norm rows, rows equal each sequence embedded
+    alone bit for bit, two rows match the oracle."""
+    e, o = models(full_spec, synth.CONFIG_MIX[3], synth.CONFIG_SEED + 3)
+    ids, mask = synth.config_inputs(3)
+    B, L = ids.shape
+    lens = mask.sum(axis=1)
+    assert (B, L) == (64, 128)
+    batch = e.embed_padded(ids, mask)
+    assert np.all(np.isfinite(batch))
+    assert np.abs(np.linalg.norm(batch.astype(np.float64), axis=1) - 1.0).max() < 1e-5
+    picks = sorted({int(np.argmin(lens)), int(np.argmax(lens)), 31})
+    for i in picks:
+        assert np.array_equal(bits(e.embed(ids[i, :lens[i]])), bits(batch[i])), i
+    compare(batch[picks[:2]], np.stack([o.embed(ids[i, :lens[i]]) for i in picks[:2]]), "c3 full size")
+
+
 def test_config5_full_size_properties(gpu, full_spec):
     """Config 5 at its full size (full 12-layer Q8_0 model, B=8, lengths in [1024, 2048] padded
     to 2048): finite unit-norm rows, rows equal each sequence embedded alone bit for bit, the
