@@ -151,8 +151,15 @@ int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t
  * 1 = a token id was out of range (clamped), 2 = a packed batch's offsets were inconsistent. */
 int32_t lle_model_status(lle_model* m, int32_t* status);
 
-/* Kernel timing: enable (1) / disable (0) and read per-kernel-class HIP-event totals. */
+/* Kernel timing: enable (1) / disable (0) and read per-kernel-class HIP-event totals.
+ * lle_model_set_timing brackets every launch and synchronises at the end of each forward.
+ * lle_model_set_timing_kernel brackets only the launches of one kernel class (e.g. "gemm_upgate";
+ * NULL or "" disables timing) and does not synchronise per forward: its events are read by
+ * lle_model_get_timing, which waits for the device. Both run forwards eagerly (no graph replay).
+ * No counterpart in the reference (SgemmInfo, internal/ggml/sgemm.go:263-269, is its only
+ * introspection); used by the benchmark. */
 int32_t lle_model_set_timing(lle_model* m, int32_t enable);
+int32_t lle_model_set_timing_kernel(lle_model* m, const char* kernel_class);
 int32_t lle_model_get_timing(lle_model* m, lle_kernel_time* out, int32_t cap, int32_t* n_out);
 
 /* Isolated quantised projection (gemmOrBatch, internal/embed/bert.go:579-638):

@@ -103,6 +103,7 @@ struct lle_model {
   bool use_graphs = true;
   // timing
   bool timing = false;
+  std::string timing_only;  // non-empty: only this kernel class is bracketed, read at get_timing
   std::vector<lle::Timer> pending;
   std::vector<lle_kernel_time> totals;
   std::vector<hipEvent_t> event_pool;
@@ -198,7 +199,8 @@ struct Scope {
   hipStream_t st;
   Timer t;
   bool on;
-  Scope(lle_model* m_, hipStream_t st_, const char* name, double flops, double bytes) : m(m_), st(st_), on(m_->timing) {
+  Scope(lle_model* m_, hipStream_t st_, const char* name, double flops, double bytes)
+      : m(m_), st(st_), on(m_->timing && (m_->timing_only.empty() || m_->timing_only == name)) {
     if (on) {
       t.name = name;
       t.flops = flops;
@@ -518,7 +520,7 @@ static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B
   if (hidden) LLE_HIP(hipMemcpyAsync(hidden, m->h, T * m->D * 4, hipMemcpyDeviceToHost, st));
   // host buffers above (pids, prow, soff, ones) must outlive the copies
   LLE_HIP(hipStreamSynchronize(st));
-  if (m->timing) collect_timing(m);
+  if (m->timing && m->timing_only.empty()) collect_timing(m);
   return LLE_OK;
 }
 
@@ -934,7 +936,7 @@ int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t*
   if ((rc = ensure_ws(m, B, L))) return rc;
   hipStream_t st = stream ? (hipStream_t)stream : m->stream;
   if ((rc = run_forward(m, d_ids, d_mask, B, L, out_dim, d_out, st))) return rc;
-  if (m->timing) {
+  if (m->timing && m->timing_only.empty()) {
     LLE_HIP(hipStreamSynchronize(st));
     collect_timing(m);
   }
@@ -955,7 +957,7 @@ int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t
   LAUNCH(launch_pack_tables(d_seq_off, B, T, L, m->seq_off, m->tokrow, m->mask, m->status, st));
   Packing pk{T, m->tokrow, m->seq_off};
   if ((rc = run_forward(m, d_ids, m->mask, B, L, out_dim, d_out, st, &pk))) return rc;
-  if (m->timing) {
+  if (m->timing && m->timing_only.empty()) {
     LLE_HIP(hipStreamSynchronize(st));
     collect_timing(m);
   }
@@ -974,14 +976,35 @@ int32_t lle_model_status(lle_model* m, int32_t* status) {
 int32_t lle_model_set_timing(lle_model* m, int32_t enable) {
   if (!m) return fail(LLE_EINVAL, "null model");
   std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  LLE_HIP(hipDeviceSynchronize());
+  collect_timing(m);  // events of an earlier single-class run
   m->timing = enable != 0;  // timed forwards run eagerly (events around every launch)
+  m->timing_only.clear();
   m->totals.clear();
+  return LLE_OK;
+}
+
+int32_t lle_model_set_timing_kernel(lle_model* m, const char* kernel_class) {
+  if (!m) return fail(LLE_EINVAL, "null model");
+  std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  LLE_HIP(hipDeviceSynchronize());
+  collect_timing(m);
+  m->totals.clear();
+  m->timing = kernel_class && kernel_class[0];
+  m->timing_only = m->timing ? std::string(kernel_class) : std::string();
   return LLE_OK;
 }
 
 int32_t lle_model_get_timing(lle_model* m, lle_kernel_time* out, int32_t cap, int32_t* n_out) {
   if (!m || !n_out) return fail(LLE_EINVAL, "null argument");
   std::lock_guard<std::mutex> lk(m->mu);
+  if (!m->pending.empty()) {  // single-class mode reads its events here, after the forwards end
+    LLE_HIP(hipSetDevice(m->device));
+    LLE_HIP(hipDeviceSynchronize());
+    collect_timing(m);
+  }
   const int n = (int)m->totals.size();
   for (int i = 0; i < n && i < cap && out; i++) out[i] = m->totals[i];
   *n_out = n;

@@ -17,7 +17,7 @@ EXPORTS = [
     "lle_abi_version", "lle_init", "lle_last_error", "lle_info", "lle_f16_to_f32", "lle_dequant",
     "lle_model_create", "lle_model_load_gguf", "lle_model_destroy", "lle_model_dims", "lle_embed",
     "lle_embed_batch", "lle_embed_batch_async", "lle_forward_hidden", "lle_model_status",
-    "lle_model_set_timing", "lle_model_get_timing", "lle_weight_create", "lle_weight_destroy",
+    "lle_model_set_timing", "lle_model_set_timing_kernel", "lle_model_get_timing", "lle_weight_create", "lle_weight_destroy",
     "lle_weight_dequant", "lle_weight_dequant_f16", "lle_gemm", "lle_gemm_async", "lle_gemm_f16_async",
     "lle_tokenizer_load_gguf", "lle_tokenizer_create", "lle_tokenizer_destroy", "lle_tokenizer_vocab_size",
     "lle_tokenize", "lle_tokenize_batch", "lle_embed_texts", "lle_embed_packed_async",
@@ -80,6 +80,7 @@ def lib(path: str | None = None):
         "lle_forward_hidden": ([P, P, P, I32, I32, P], I32),
         "lle_model_status": ([P, P], I32),
         "lle_model_set_timing": ([P, I32], I32),
+        "lle_model_set_timing_kernel": ([P, C.c_char_p], I32),
         "lle_model_get_timing": ([P, C.POINTER(KernelTime), I32, P], I32),
         "lle_weight_create": ([I32, P, I32, I32, C.POINTER(P)], I32),
         "lle_weight_destroy": ([P], I32),

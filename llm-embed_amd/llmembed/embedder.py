@@ -56,6 +56,10 @@ class BertModel:
     def set_timing(self, on: bool):
         check(_lib.lib().lle_model_set_timing(self.h, 1 if on else 0))
 
+    def set_timing_kernel(self, kernel_class: str | None):
+        """Time only the launches of one kernel class (no per-forward synchronisation)."""
+        check(_lib.lib().lle_model_set_timing_kernel(self.h, kernel_class.encode() if kernel_class else None))
+
     def timing(self) -> dict:
         n = C.c_int32()
         arr = (_lib.KernelTime * 64)()

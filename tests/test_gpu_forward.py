@@ -299,6 +299,31 @@ def test_graph_replay_matches_eager(gpu, small_spec):
     compare(e.embed(a), o.embed(a), "graph replay")
 
 
+def test_single_class_timing(gpu, small_spec):
+    """lle_model_set_timing_kernel brackets only one kernel class, with no synchronisation per
+    forward: its totals hold exactly that class's launches (one per layer per forward) and the
+    rows equal untimed forwards bit for bit."""
+    e, _ = models(small_spec, "Q8_0")
+    rng = np.random.default_rng(37)
+    ids = rng.integers(0, small_spec.vocab, (40, 128)).astype(np.int32)  # 5120 tokens: eager
+    m = e.model()
+    ref = e.embed_padded(ids, np.ones_like(ids))
+    m.set_timing_kernel("gemm_upgate")
+    outs = [e.embed_padded(ids, np.ones_like(ids)) for _ in range(3)]
+    kt = m.timing()
+    m.set_timing_kernel(None)
+    assert set(kt) == {"gemm_upgate"}
+    assert kt["gemm_upgate"]["launches"] == 3 * small_spec.n_layer
+    assert kt["gemm_upgate"]["total_ms"] > 0
+    for o_ in outs:
+        assert np.array_equal(bits(o_), bits(ref))
+    m.set_timing(True)
+    e.embed_padded(ids, np.ones_like(ids))
+    kt = m.timing()
+    m.set_timing(False)
+    assert {"gemm_qkv", "attention", "gemm_upgate"} <= set(kt)
+
+
 @pytest.mark.parametrize("B,L,seed", [(3, 8, 1), (4, 20, 2), (5, 40, 3), (12, 100, 4), (20, 128, 5)])
 def test_packed_rows_equal_padded_forward(gpu, small_spec, B, L, seed):
     """lle_embed_batch (host pointers) drops the positions after each row's last valid token;
