@@ -209,21 +209,26 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
         }
         st[t] = acc;
       }
+      // u = unscaled score; the reference's s = u * scale is exact (a power of two), so s is
+      // never formed: a masked key gets u = -8e9 (u * scale = -1e9 exactly), maxima and minima
+      // are taken on u and scaled afterwards, and s - m is fmaf(u, scale, -m), whose single
+      // rounding is that of the subtraction.
       float s[16];
 #pragma unroll
       for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) s[4 * t + r] = st[t][r] * scale;
+        for (int r = 0; r < 4; r++) s[4 * t + r] = st[t][r];
       if (!sFull[buf]) {  // masked (and out-of-range) keys; tiles of valid keys skip the lookups
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
           for (int r = 0; r < 4; r++)
-            if (sMask[buf][32 * (t >> 1) + 8 * g + 4 * (t & 1) + r] == 0) s[4 * t + r] = -1e9f;
+            if (sMask[buf][32 * (t >> 1) + 8 * g + 4 * (t & 1) + r] == 0) s[4 * t + r] = -8e9f;
       }
       float tmax = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, s[i]);
+      tmax *= scale;
       float alpha = 1.f, mref;
       if (!fixed) {
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
@@ -239,7 +244,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
       float ps = 0.f;
 #pragma unroll
       for (int i = 0; i < 16; i++) {  // branch-free: exp of a dropped key (z < -10) is discarded
-        const float z = s[i] - mref;
+        const float z = fmaf(s[i], scale, -mref);
         const bool keep = z >= -10.f;
         const float ex = __expf(z);
         e[i] = keep ? ex : 0.f;
@@ -269,7 +274,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
     }
     if (!fixed) {
       float sm = fminf(smin, __shfl_xor(smin, 16));
-      sm = fminf(sm, __shfl_xor(sm, 32));
+      sm = fminf(sm, __shfl_xor(sm, 32)) * scale;
       const bool flag = qvalid && (sm - m_run < -10.f);
       if (__any(flag)) sRedo = 1;  // benign race: every writer stores 1
     }
