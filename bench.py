@@ -431,6 +431,30 @@ def main():
                            f"{min(os.cpu_count() or 1, 8)} GEMM threads, {cs:.1f} s wall on {ncores} available cores"),
                    gpu_vs_cpu_min_cos=float(cos.min()))
         log(f"[bench] cpu oracle {S / cs:.2f} emb/s ({cs:.1f} s); min cos vs GPU {cos.min():.7f}")
+        # host CPU identity, and config 1 on the CPU: p50 wall time of one L=8 sequence over 50 runs
+        model_name, avx512 = None, None
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name") and model_name is None:
+                        model_name = line.split(":", 1)[1].strip()
+                    elif line.startswith("flags") and avx512 is None:
+                        avx512 = "avx512f" in line.split()
+        except OSError:
+            pass
+        cpu.update(cpu_model=model_name, avx512f=avx512, nproc=os.cpu_count(), affinity_cores=ncores)
+        if args.latency_iters > 0:
+            om.embed(ids1[0], mask1[0])
+            ts = []
+            for _ in range(50):
+                a = time.perf_counter()
+                v1c = om.embed(ids1[0], mask1[0])
+                ts.append(time.perf_counter() - a)
+            cpu["c1_p50_ms"] = 1e3 * float(np.percentile(ts, 50))
+            cpu["c1_sample"] = (f"config 1 (B=1, L={L1}) through the same C oracle, {min(os.cpu_count() or 1, 8)} "
+                                "GEMM threads, p50 wall over 50 runs after one warm-up")
+            log(f"[bench] cpu oracle c1 p50 {cpu['c1_p50_ms']:.2f} ms; cos vs GPU "
+                f"{float(np.dot(v1c, v1) / np.linalg.norm(v1c) / np.linalg.norm(v1)):.7f}")
 
     res = {
         "metric": "embeddings/sec at B=256,L=128 Q8_0",

@@ -248,7 +248,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
         const bool keep = z >= -10.f;
         const float ex = __expf(z);
         e[i] = keep ? ex : 0.f;
-        smin = keep ? fminf(smin, s[i]) : smin;
+        smin = fminf(smin, keep ? s[i] : INFINITY);  // independent selects: min3 chains
         ps += e[i];
       }
       lsum = lsum * alpha + ps;
