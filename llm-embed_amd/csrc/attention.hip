@@ -34,6 +34,24 @@ __device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const 
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Raw buffer of nbytes at base (loads at offsets >= nbytes return zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nbytes, 0x00020000);
+}
+// A wave-uniform pointer moved to scalar registers (64-bit products are formed on the VALU, and
+// a buffer descriptor built from VGPRs turns every load into a readfirstlane loop).
+__device__ __forceinline__ const __half* uniform_ptr(const __half* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const __half*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) {
+  const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+  return uint4{t.x, t.y, t.z, t.w};
+}
+
 // NW waves per block (16 queries each). K / V^T tiles are double-buffered: the global loads of
 // key tile kt+1 are issued before tile kt's MFMAs and land in the other LDS buffer afterwards.
 template <int NW, bool EARLY>
@@ -54,7 +72,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
   const int q = qt * AQB + wave * 16 + lr;
   // positions of this sequence held in Q / K / V^T: all L, or (packed rows) up to its last
   // valid token; keys and queries past them are zero / not written
-  const int Lk = a.seq_off ? a.seq_off[b + 1] - a.seq_off[b] : L;
+  const int Lk = __builtin_amdgcn_readfirstlane(a.seq_off ? a.seq_off[b + 1] - a.seq_off[b] : L);  // uniform
   const size_t orow = a.seq_off ? (size_t)a.seq_off[b] : (size_t)b * L;
   // only valid (mask 1) queries may ask for the fixed-max pass: padding queries' outputs are
   // never used, and the pass decision must not depend on how a sequence was padded
@@ -72,23 +90,33 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
 
   uint4 kreg[CPT], vreg[CPT];
   int mreg = 0;
+  // K and V^T tiles through buffer loads: the per-lane byte offsets are fixed and a tile adds
+  // one constant. K's buffer is this head's first Lk rows, so rows at and past Lk read as zero
+  // (range check); every visited tile lies below Lp, so each load is inside the allocation.
+  // V^T's columns at and past Lk are never written and are zeroed in the tile that holds Lk.
+  const __half* const kbase = uniform_ptr(a.k + head * Lp * HD);
+  const __half* const vbase = uniform_ptr(a.vt + head * HD * Lp);
+  int koff[CPT], voff[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; i++) {
+    const int c = tid + i * NT, row = c >> 3, ch = c & 7;
+    koff[i] = (row * HD + ch * 8) * 2;
+    voff[i] = (row * Lp + ch * 8) * 2;
+  }
   auto gload = [&](int kt) {
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, Lk * HD * 2);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, HD * Lp * 2);
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
-      const int c = tid + i * NT, row = c >> 3, ch = c & 7;
-      const int key = kt * AK + row;
-      kreg[i] = key < Lk ? *(const uint4*)(a.k + (head * Lp + key) * HD + ch * 8) : uint4{0, 0, 0, 0};
-      const int k0 = kt * AK + ch * 8;
-      uint4 vv = uint4{0, 0, 0, 0};
-      if (k0 < Lk) {
-        vv = *(const uint4*)(a.vt + (head * HD + row) * Lp + k0);
-        if (k0 + 8 > Lk) {  // zero the keys at and past Lk (columns never written)
-          const int nv = Lk - k0;
-          vv.x &= (nv > 0 ? 0xFFFFu : 0u) | (nv > 1 ? 0xFFFF0000u : 0u);
-          vv.y &= (nv > 2 ? 0xFFFFu : 0u) | (nv > 3 ? 0xFFFF0000u : 0u);
-          vv.z &= (nv > 4 ? 0xFFFFu : 0u) | (nv > 5 ? 0xFFFF0000u : 0u);
-          vv.w &= (nv > 6 ? 0xFFFFu : 0u) | (nv > 7 ? 0xFFFF0000u : 0u);
-        }
+      kreg[i] = buf_load16(rk, koff[i] + kt * (AK * HD * 2));
+      uint4 vv = buf_load16(rv, voff[i] + kt * (AK * 2));
+      if ((kt + 1) * AK > Lk) {  // wave-uniform: the tile that holds Lk (or lies past it)
+        const int c = tid + i * NT, ch = c & 7;
+        const int nv = Lk - (kt * AK + ch * 8);
+        vv.x &= (nv > 0 ? 0xFFFFu : 0u) | (nv > 1 ? 0xFFFF0000u : 0u);
+        vv.y &= (nv > 2 ? 0xFFFFu : 0u) | (nv > 3 ? 0xFFFF0000u : 0u);
+        vv.z &= (nv > 4 ? 0xFFFFu : 0u) | (nv > 5 ? 0xFFFF0000u : 0u);
+        vv.w &= (nv > 6 ? 0xFFFFu : 0u) | (nv > 7 ? 0xFFFF0000u : 0u);
       }
       vreg[i] = vv;
     }
