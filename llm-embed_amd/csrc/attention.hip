@@ -54,8 +54,9 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) 
 
 // NW waves per block (16 queries each). K / V^T tiles are double-buffered: the global loads of
 // key tile kt+1 are issued before tile kt's MFMAs and land in the other LDS buffer afterwards.
+// The 8-wave kernel is held to 128 VGPRs (4 waves per SIMD, two blocks per CU).
 template <int NW, bool EARLY>
-__global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(AttnArgs a) {
   constexpr int NT = NW * 64, AQB = NW * 16;
   constexpr int CPT = (AK * HD / 8) / NT;  // 16-byte chunks of each tile per thread
   __shared__ __attribute__((aligned(16))) _Float16 sK[2][AK][HD + APAD];   // [key][dim]
@@ -291,10 +292,18 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnArgs a) {
           pf[r] = (_Float16)e[4 * (2 * j) + r];
           pf[4 + r] = (_Float16)e[4 * (2 * j + 1) + r];
         }
+        if constexpr (NW == 8) {  // the four V^T fragment reads issued together, then the MFMAs
+          half8 vf[4];
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-          const half8 vf = *(const half8*)&sV[buf][dt * 16 + lr][32 * j + 8 * g];
-          o[dt] = mfma16(vf, pf, o[dt]);
+          for (int dt = 0; dt < 4; dt++) vf[dt] = *(const half8*)&sV[buf][dt * 16 + lr][32 * j + 8 * g];
+#pragma unroll
+          for (int dt = 0; dt < 4; dt++) o[dt] = mfma16(vf[dt], pf, o[dt]);
+        } else {  // one read per MFMA: keeps the 4-wave kernel at 3 waves per SIMD
+#pragma unroll
+          for (int dt = 0; dt < 4; dt++) {
+            const half8 vf = *(const half8*)&sV[buf][dt * 16 + lr][32 * j + 8 * g];
+            o[dt] = mfma16(vf, pf, o[dt]);
+          }
         }
       }
       if (more) sstore(buf ^ 1);  // buffer buf^1 was last read in iteration kt-1
