@@ -194,6 +194,8 @@ static hipEvent_t get_event(lle_model* m) {
   return e;
 }
 
+static void collect_timing(lle_model* m);
+
 struct Scope {
   lle_model* m;
   hipStream_t st;
@@ -214,6 +216,12 @@ struct Scope {
     if (on) {
       (void)hipEventRecord(t.b, st);
       m->pending.push_back(t);
+      // single-class mode reads its events at lle_model_get_timing; a caller that never reads
+      // them is bounded here (the totals keep accumulating)
+      if (m->pending.size() >= 4096) {
+        (void)hipStreamSynchronize(st);
+        collect_timing(m);
+      }
     }
   }
 };
