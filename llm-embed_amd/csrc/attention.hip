@@ -277,7 +277,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
         const bool keep = z >= -10.f;
         const float ex = __expf(z);
         e[i] = keep ? ex : 0.f;
-        smin = fminf(smin, keep ? s[i] : INFINITY);  // independent selects: min3 chains
+        smin = fminf(smin, keep ? s[i] : INFINITY);  // smallest kept score (exact, order-free)
         ps += e[i];
       }
       lsum = lsum * alpha + ps;
