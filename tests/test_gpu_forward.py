@@ -356,6 +356,38 @@ def test_packed_rows_equal_padded_forward(gpu, small_spec, B, L, seed):
     compare(host[1:], o.embed_batch(ids[1:], mask[1:]), f"packed B={B} L={L}")
 
 
+def test_key_tile_boundaries(gpu, small_spec):
+    """Sequences whose last stored key falls exactly on, just past, and well inside a 64-key
+    tile (lengths 64, 128, 65, 192 and 1 in a batch padded to 192): the attention reads K tiles
+    bounded at that key and zeroes V^T's columns only in the tile that holds it. The padded
+    device entry (every position stored), the packed host entry (positions past each sequence's
+    last valid token dropped) and single-sequence embeds agree bit for bit, and match the
+    oracle."""
+    from llmembed import _hip
+    from llmembed._lib import check, lib
+
+    e, o = models(small_spec, "Q8_0")
+    D = small_spec.d_model
+    lens = [64, 128, 65, 192, 1]
+    B, L = len(lens), 192
+    rng = np.random.default_rng(53)
+    ids = rng.integers(0, small_spec.vocab, (B, L)).astype(np.int32)
+    mask = np.zeros((B, L), np.int32)
+    for b, n in enumerate(lens):
+        mask[b, :n] = 1
+    print(f"key tiles: lengths {lens} padded to {L}", flush=True)
+    host = e.embed_padded(ids, mask)
+    di, dm = _hip.DeviceBuffer.from_array(ids), _hip.DeviceBuffer.from_array(mask)
+    do = _hip.DeviceBuffer(B * D * 4)
+    check(lib().lle_embed_batch_async(e.model().h, di.ptr, dm.ptr, B, L, D, do.ptr, None))
+    _hip.synchronize()
+    dev = do.download((B, D), np.float32)
+    assert np.array_equal(bits(host), bits(dev))
+    for b, n in enumerate(lens):
+        assert np.array_equal(bits(e.embed(ids[b, :n])), bits(host[b])), lens[b]
+    compare(host, o.embed_batch(ids, mask), "key tile boundaries")
+
+
 @pytest.mark.parametrize("qkv_std", [0.02, 0.3])
 def test_small_batch_schedule_bitexact(gpu, small_spec, qkv_std):
     """Batches of <= 16 rows run the small-batch schedule (LayerNorms inside the consuming GEMMs,
