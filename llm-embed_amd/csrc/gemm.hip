@@ -534,6 +534,48 @@ __device__ __forceinline__ void qkv_tile(const GemmP& p, const floatx4 (&acc)[FB
   }
 }
 
+// qkv_tile with the RoPE cos / sin rows of the block's 256 tokens staged in LDS (rope: cos rows
+// [256][32] f32, then sin rows; logical 16-byte chunk c of row r at slot c ^ (r & 7)) instead of
+// held in registers; rl0 is the wave tile's first row in the block. Same arithmetic and stores.
+template <int FB, int TB>
+__device__ __forceinline__ void qkv_tile_lds(const GemmP& p, const floatx4 (&acc)[FB][TB], const float* rope,
+                                             const int (&bs)[TB], const int (&ps)[TB], int rl0, int mb, int fb,
+                                             int lane) {
+  const int lr = lane & 15, lg = lane >> 4;
+  const int D = p.D, Lp = p.Lp, H = p.H, M = p.M;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q), rk = make_rsrc(p.k), rv = make_rsrc(p.vt);
+#pragma unroll
+  for (int i = 0; i < FB; i++) {
+    const int f0 = fb + i * 16;  // wave-uniform
+    const int sec = f0 >= 2 * D ? 2 : (f0 >= D ? 1 : 0);
+    const int fi = f0 - sec * D + lg * 4, h = fi >> 6, e = fi & 63;
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+      if (mb + j * 16 + lr >= M) continue;
+      floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+      v += acc[i][j];  // total = 0 + chunk
+      if (sec < 2) {
+        const int rl = rl0 + j * 16 + lr;
+        const int o = rl * 32 + (((e >> 3) ^ (rl & 7)) << 2) + ((e >> 1) & 3);  // floats e/2, e/2 + 1
+        const float2 c = *(const float2*)(rope + o);
+        const float2 sn = *(const float2*)(rope + 256 * 32 + o);
+        const float c0 = c.x, s0 = sn.x, c1 = c.y, s1 = sn.y;
+        const float a0 = v.x * c0 - v.y * s0, a1 = v.x * s0 + v.y * c0;
+        const float a2 = v.z * c1 - v.w * s1, a3 = v.z * s1 + v.w * c1;
+        const __half2 lo = __floats2half2_rn(a0, a1), hi = __floats2half2_rn(a2, a3);
+        const int off = (((bs[j] * H + h) * Lp + ps[j]) * 64 + e) * 2;
+        st_b64(sec == 0 ? rq : rk, off, __builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+      } else {
+        const int off = (((bs[j] * H + h) * 64 + e) * Lp + ps[j]) * 2;
+        st_b16(rv, off, __float2half_rn(v.x));
+        st_b16(rv, off + Lp * 2, __float2half_rn(v.y));
+        st_b16(rv, off + Lp * 4, __float2half_rn(v.z));
+        st_b16(rv, off + Lp * 6, __float2half_rn(v.w));
+      }
+    }
+  }
+}
+
 // LDS rows are 64 bytes (4 chunks of 16 B); chunk c of row r sits at c ^ swr(r), which spreads
 // a 16-row fragment read over all banks.
 __device__ __forceinline__ int swr(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
@@ -588,7 +630,7 @@ __device__ __forceinline__ void xcd_tile(int& m0, int& n0) {
     const int ntl = nt / NG, mtl = mt / MG;
     n0 = ((xcd % NG) * ntl + slot % ntl) * BN;
     m0 = ((xcd / NG) * mtl + slot / ntl) * BM;
-  } else if (NG == 1) {
+  } else {  // each XCD takes a contiguous run of the row-major tile order
     const int q = G >> 3, r = G & 7;
     const int t = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
     n0 = (t % nt) * BN;
@@ -636,13 +678,19 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   // The RoPE epilogue's cos/sin pairs are loaded before the K loop (their latency then hides
   // behind it; issued after the first LDS-DMA loads would break the vmcnt accounting below,
   // which counts on every older memory operation being complete). Rows past M load row M-1.
-  constexpr bool PRE = EPI == EPI_QKV;
+  // 256 x 256 QKV tiles (one section each: D % 256 == 0) cannot hold these operands beside
+  // their accumulators; their cos / sin rows are brought into the stage the last K step leaves
+  // free (ROPE_LDS) and read from LDS in the epilogue.
+  constexpr bool QKV = EPI == EPI_QKV && !MULTI;
+  constexpr bool ROPE_LDS = QKV && BM == 256 && BN == 256 && NS == 2;
+  constexpr bool PRE = EPI == EPI_QKV && !ROPE_LDS;
   floatx4 eop[PRE ? FB : 1][PRE ? TB : 1];
-  int qb[PRE ? TB : 1], qp[PRE ? TB : 1];
+  int qb[(PRE || QKV) ? TB : 1], qp[(PRE || QKV) ? TB : 1];
   if constexpr (PRE) {
     qkv_rows<TB>(p, m0 + wm * TM, lane, qb, qp);
     qkv_rope_operands<FB, TB>(p, qp, n0 + wn * TN, lane, eop);
   }
+  const int rsec = n0 >= 2 * p.D ? 2 : (n0 >= p.D ? 1 : 0);  // ROPE_LDS: the tile's section
 
   // loop-invariant byte offsets; the K step advances in the scalar offset. Rows past M re-read
   // row M-1 (they only feed output rows that are never stored).
@@ -716,7 +764,26 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + NS - 1 < KT) issue(SN, kt + NS - 1);
+    if (kt + NS - 1 < KT) {
+      issue(SN, kt + NS - 1);
+    } else if constexpr (ROPE_LDS) {
+      if (kt == KT - 1 && rsec < 2) {  // SN (stage 0) was last read by step kt - 1
+        // instruction j of wave w fills tile rows (4 w + j) * 8 + lane / 8 with the cos / sin
+        // row of that token's position (rows past M: row M - 1), the lane fetching the logical
+        // 16-byte chunk (lane % 8) ^ (row & 7)
+        const u32x4_sgpr rc = rsrc_words(p.rope_cos), rs = rsrc_words(p.rope_sin);
+        float* rope = (float*)(smem + decltype(SN)::value * STAGE);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int r = (wave * 4 + j) * 8 + (lane >> 3);
+          const int m = min(m0 + r, M - 1);
+          const int t = p.tokrow ? p.tokrow[m] : m;
+          const int ro = ((t - (t / p.L) * p.L) * 32 + (((lane & 7) ^ (r & 7)) << 2)) * 4;
+          dma16(rc, rope + (wave * 4 + j) * 8 * 32, ro, 0);
+          dma16(rs, rope + 256 * 32 + (wave * 4 + j) * 8 * 32, ro, 0);
+        }
+      }
+    }
     compute(S, kt);
   };
   issue(S0{}, 0);
@@ -730,6 +797,17 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
       step(S1{}, S0{}, kt + 1);
       step(S2{}, S1{}, kt + 2);
     }
+  }
+  if constexpr (ROPE_LDS) {
+    qkv_rows<TB>(p, m0 + wm * TM, lane, qb, qp);
+    if (rsec < 2) {  // wave-uniform: every wave's RoPE rows have landed
+      __builtin_amdgcn_s_waitcnt(0);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+    qkv_tile_lds<FB, TB>(p, acc, (const float*)smem, qb, qp, wm * TM, m0 + wm * TM, n0 + wn * TN, lane);
+    return;
   }
 
   if constexpr (EPI == EPI_GEGLU && BM == 256 && BN == 256 && WM == 4 && WN == 2 && !MULTI) {
@@ -808,7 +886,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     }
     return;
   }
-  tile_epilogue<EPI, MULTI, FB, TB>(p, acc, tot, eop, qb, qp, m0 + wm * TM, n0 + wn * TN, lane);
+  if constexpr (!ROPE_LDS) tile_epilogue<EPI, MULTI, FB, TB>(p, acc, tot, eop, qb, qp, m0 + wm * TM, n0 + wn * TN, lane);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1364,6 +1442,14 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
       dim3 grid(p.N / 256, (p.M + 255) / 256);
       hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
       return hipGetLastError();
+    }
+    if constexpr (EPI == EPI_QKV) {
+      if (!multi && p.N % 256 == 0 && p.D % 256 == 0 && (p.K / KSTEP) % 2 == 0) {
+        // 256 x 256 tiles, 2 stages of 64 KB, RoPE operands staged in LDS after the K loop
+        dim3 grid(p.N / 256, (p.M + 255) / 256);
+        hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
+        return hipGetLastError();
+      }
     }
     if ((p.K / KSTEP) % 3 == 0) {
       dim3 grid(p.N / 128, (p.M + 255) / 256);  // 3 stages of 48 KB
