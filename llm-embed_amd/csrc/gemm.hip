@@ -1438,7 +1438,8 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
   const bool multi = p.K > kchunk_of(p.K);
   if (p.M < 1024 && (!multi || p.part)) return launch_small<FMT, 64, EPI>(p, st, reduce);
   if (p.M >= 1024 && p.w16) {
-    if (!multi && p.N >= 4096 && p.N % 256 == 0) {  // 2 stages of 64 KB
+    // 2 stages of 64 KB; f32 outputs from N = 2048 (fewer N tiles leave a round mostly empty)
+    if (!multi && p.N % 256 == 0 && (p.N >= 4096 || (EPI == EPI_F32 && p.N >= 2048))) {
       dim3 grid(p.N / 256, (p.M + 255) / 256);
       hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
       return hipGetLastError();
