@@ -50,6 +50,30 @@ def test_embed_small_model(gpu, small_spec, mix):
         compare(e.embed(ids), o.embed(ids), f"{mix} L={L}")
 
 
+@pytest.mark.parametrize("mix", ["Q8_0", "Q4_K", "Q5_K", "Q6_K", "F32", "Q5_K_M"])
+def test_large_batch_formats(gpu, small_spec, mix):
+    """A batch of >= 1024 packed rows (12 sequences of ragged length, host entry) runs the
+    large-batch GEMMs on the resident f16 weight copies: QKV on 256 x 256 tiles with its RoPE
+    operands staged in LDS (row positions through the packed-row map), up||gate, down and the
+    full-row out projection. Every row equals the sequence embedded alone (the small-batch
+    schedule) bit for bit, and the rows match the oracle."""
+    e, o = models(small_spec, mix)
+    rng = np.random.default_rng(61)
+    B, L = 12, 128
+    ids = rng.integers(0, small_spec.vocab, (B, L)).astype(np.int32)
+    lens = rng.integers(88, L + 1, B)
+    lens[0] = L
+    mask = np.zeros((B, L), np.int32)
+    for b in range(B):
+        mask[b, :lens[b]] = 1
+    print(f"large batch {mix}: {int(lens.sum())} rows", flush=True)
+    assert lens.sum() >= 1024
+    batch = e.embed_padded(ids, mask)
+    for b in (0, 5, 11):
+        assert np.array_equal(bits(e.embed(ids[b, :lens[b]])), bits(batch[b])), (mix, b)
+    compare(batch, o.embed_batch(ids, mask), f"large batch {mix}")
+
+
 def test_config1_full_model(gpu, full_spec):
     """Config 1: full 12-layer Q8_0 model, B=1, L=8."""
     e, o = models(full_spec, "Q8_0", synth.CONFIG_SEED + 1)
