@@ -59,9 +59,10 @@ def main():
     ap.add_argument("--probe-traffic", action="store_true",
                     help="for rocprofv3 --pmc runs: two config-4 forwards, then one 256 MiB device-to-device copy "
                          "(the calibration of FETCH_SIZE / WRITE_SIZE); prints no JSON")
-    ap.add_argument("--probe-config", type=int, default=4, choices=(3, 4, 5),
+    ap.add_argument("--probe-config", type=int, default=4, choices=(1, 3, 4, 5),
                     help="with --probe-traffic: the configuration whose two forwards are run (padded batch, "
-                         "device-pointer entry)")
+                         "device-pointer entry); config 1 runs 30 forwards rotated over three model copies "
+                         "(the cold-MALL latency setting) after 30 warm-ups")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); sequences are "
@@ -96,6 +97,16 @@ def main():
         if args.probe_config == 4:
             step()
             step()
+        elif args.probe_config == 1:
+            ids1, mask1 = synth.config_inputs(1)
+            d_i1, d_m1 = _hip.DeviceBuffer.from_array(ids1), _hip.DeviceBuffer.from_array(mask1)
+            d_o1 = _hip.DeviceBuffer(D * 4)
+            cps = [model] + [llmembed.Embedder.load(path).model() for _ in range(2)]
+            for i in range(60):  # 30 warm-ups (graph capture), then the 30 forwards a trace reads
+                check(L_.lle_embed_batch_async(cps[i % 3].h, d_i1.ptr, d_m1.ptr, 1, ids1.shape[1], D, d_o1.ptr,
+                                               stream.h))
+                stream.synchronize()
+            log("[bench] config-1 probe: 60 forwards (the last 30 after warm-up), rotated over 3 model copies")
         else:
             ids_p, mask_p = synth.config_inputs(args.probe_config)
             mp = llmembed.Embedder.load(synth.model_path(spec, synth.CONFIG_MIX[args.probe_config],
@@ -308,7 +319,9 @@ def main():
         # M in {8, 512, 32768}, four formats; X f16 resident on the device (lle_gemm_f16_async),
         # device time per call from HIP events (median of 20); for M = 8 also a back-to-back
         # sequence over distinct weight copies (HBM streaming). Roofline: the dense fp16 MFMA peak
-        # for FLOP/s, and for bytes the quantised W + X f16 + Y f32 read/written once.
+        # for FLOP/s, and for bytes the quantised W + X f16 + Y f32 read/written once. For
+        # M >= 512 also the call as config 2 states it, on f32 X in HBM (lle_gemm_async: the
+        # f32 -> f16 pass, then the GEMM), with bytes W + X f32 + Y f32.
         from llmembed import quant as q_
 
         c2 = []
@@ -316,8 +329,10 @@ def main():
         xbuf = _hip.DeviceBuffer(32768 * 3072 * 2)
         ybuf = _hip.DeviceBuffer(32768 * 3072 * 4)
         pbuf = _hip.DeviceBuffer(4 * 1024 * 3072 * 4)  # split-K partials below 1024 rows
-        xbuf_h = (rng2.standard_normal(32768 * 3072) * 1.0).astype(np.float16)
-        xbuf.upload(xbuf_h)
+        xbuf_h = rng2.standard_normal(32768 * 3072, dtype=np.float32)
+        xbuf.upload(xbuf_h.astype(np.float16))
+        x32buf = _hip.DeviceBuffer.from_array(xbuf_h)  # config 2's f32 X
+        del xbuf_h
         e0, e1 = _hip.Event(), _hip.Event()
         for tname, t in (("Q8_0", q_.Q8_0), ("Q6_K", q_.Q6_K), ("Q5_K", q_.Q5_K), ("Q4_K", q_.Q4_K)):
             for K_c, N_c in ((768, 2304), (768, 768), (768, 3072), (3072, 768)):
@@ -340,6 +355,19 @@ def main():
                     r2 = dict(fmt=tname, K=K_c, N=N_c, M=M_c, us=1e3 * ms, tflops=flops / ms / 1e9,
                               mfma_frac=flops / ms / 1e9 / PEAK_F16_TFLOPS, gbs=nbytes / ms / 1e6,
                               hbm_frac=nbytes / ms / 1e6 / PEAK_HBM_GBS)
+                    if M_c >= 512:  # f32 X as config 2 states it
+                        def call32():
+                            W.gemm_async(x32buf.value, xbuf.value, M_c, ybuf.value, stream.h.value)
+                        call32()
+                        ts = []
+                        for _ in range(20):
+                            e0.record(stream)
+                            call32()
+                            e1.record(stream)
+                            ts.append(e0.elapsed_ms(e1))
+                        ms32 = float(np.median(ts))
+                        b32 = float(wq.nbytes) + M_c * K_c * 4 + M_c * N_c * 4
+                        r2.update(us_f32x=1e3 * ms32, tflops_f32x=flops / ms32 / 1e9, gbs_f32x=b32 / ms32 / 1e6)
                     if M_c == 8:
                         # weight streaming from HBM: back-to-back calls over distinct copies of the
                         # weight (>= 520 MB in all, past the 256 MB MALL), device time of the sequence
@@ -370,7 +398,7 @@ def main():
                     f"({100 * r['hbm_frac']:4.1f}% HBM)"
                     + (f"; back-to-back over {r['seq_copies']} weight copies {r['seq_us']:.2f} us "
                        f"{r['seq_gbs']:.0f} GB/s ({100 * r['seq_hbm_frac']:.1f}% HBM)" if "seq_us" in r else ""))
-        del xbuf, ybuf, pbuf
+        del xbuf, ybuf, pbuf, x32buf
 
         # Text path (EmbedBatch over strings): native host tokeniser, then lle_embed_texts'
         # length-ordered batches, against the same texts in input order, 256 per padded batch.
@@ -424,13 +452,16 @@ def main():
             ncores = os.cpu_count()
         workers = min(os.cpu_count() or 1, S, 8)
         cos = np.sum(ref * out[:S], axis=1) / np.linalg.norm(ref, axis=1) / np.linalg.norm(out[:S], axis=1)
+        max_abs = float(np.abs(ref.astype(np.float64) - out[:S]).max())
         cpu = dict(value=S / cs, unit="embeddings/s", cores=min(ncores, workers * min(os.cpu_count() or 1, 8)),
                    kind="port",
                    sample=(f"C oracle (restatement of the reference pure-Go AVX-512 GemmPrePacked32 path) on the first "
                            f"{S} of the {B} config-4 sequences (L={L}), {workers} EmbedBatch workers x "
                            f"{min(os.cpu_count() or 1, 8)} GEMM threads, {cs:.1f} s wall on {ncores} available cores"),
-                   gpu_vs_cpu_min_cos=float(cos.min()))
-        log(f"[bench] cpu oracle {S / cs:.2f} emb/s ({cs:.1f} s); min cos vs GPU {cos.min():.7f}")
+                   gpu_vs_cpu_min_cos=float(cos.min()), gpu_vs_cpu_max_abs=max_abs)
+        log(f"[bench] cpu oracle {S / cs:.2f} emb/s ({cs:.1f} s); vs GPU over {S} rows: min cos {cos.min():.7f}, "
+            f"max abs {max_abs:.2e}")
+        assert cos.min() >= 0.9999 and max_abs <= 1e-3, "GPU rows outside the parity bar against the oracle"
         # host CPU identity, and config 1 on the CPU: p50 wall time of one L=8 sequence over 50 runs
         model_name, avx512 = None, None
         try:

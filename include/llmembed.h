@@ -129,8 +129,11 @@ int32_t lle_embed(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t
 int32_t lle_embed_batch(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L,
                         int32_t out_dim, float* out);
 
-/* Same on device pointers, enqueued on `stream` (NULL = the model's stream); returns after
- * enqueueing. Token ids outside [0, vocab) are clamped and reported by lle_model_status. */
+/* Same on device pointers; returns after enqueueing. The forward runs on the model's own
+ * stream (its workspace is shared by every call), ordered by events after the work already
+ * queued on `stream` and before the work queued on `stream` later (NULL = the model's stream).
+ * Async work must finish before lle_model_destroy. Token ids outside [0, vocab) are clamped and
+ * reported by lle_model_status. */
 int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int32_t B,
                               int32_t L, int32_t out_dim, float* d_out, void* stream);
 
@@ -143,7 +146,7 @@ int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask
  * valid: no padding is stored or computed), d_seq_off [B+1] int32 with d_seq_off[0] = 0 and
  * d_seq_off[B] = T; L >= the longest sequence (<= context_length). Row b of d_out equals
  * lle_embed of sequence b bit for bit. Enqueued on `stream`; an inconsistent offset table is
- * made safe and reported by lle_model_status (bit 2). */
+ * made safe and reported by lle_model_status (bit 2). Stream ordering as lle_embed_batch_async. */
 int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t* d_seq_off, int32_t B, int32_t T,
                                int32_t L, int32_t out_dim, float* d_out, void* stream);
 

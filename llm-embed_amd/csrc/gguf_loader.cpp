@@ -7,7 +7,9 @@
 // ByteSize = nel / blockSize * typeSize (:196-204). Metadata keys and tensor names follow
 // LoadBertModel (internal/embed/bert.go:98-104,151-208). The file is memory-mapped for the
 // duration of the upload only.
+#include <errno.h>
 #include <fcntl.h>
+#include <stdint.h>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -74,8 +76,11 @@ bool block_geometry(uint32_t t, uint64_t* bs, uint64_t* ts) {
   return true;
 }
 
-// Skip (or keep) one typed value (readValue, reader.go:420-456).
-bool read_value(Cursor& c, uint32_t t, KV* kv) {
+// Skip (or keep) one typed value (readValue, reader.go:420-456). Arrays of arrays recurse; a
+// nesting deeper than kMaxDepth is rejected (each level costs only 12 bytes of file, so a small
+// crafted file could otherwise exhaust the stack).
+constexpr int kMaxDepth = 16;
+bool read_value(Cursor& c, uint32_t t, KV* kv, int depth = 0) {
   switch (t) {
     case 0: case 1: case 7: c.get<uint8_t>(); break;
     case 2: case 3: c.get<uint16_t>(); break;
@@ -96,10 +101,11 @@ bool read_value(Cursor& c, uint32_t t, KV* kv) {
       break;
     }
     case 9: {
+      if (depth >= kMaxDepth) return false;
       uint32_t et = c.get<uint32_t>();
       uint64_t n = c.get<uint64_t>();
       for (uint64_t i = 0; i < n && c.ok; i++)
-        if (!read_value(c, et, nullptr)) return false;
+        if (!read_value(c, et, nullptr, depth + 1)) return false;
       break;
     }
     case 10: case 11: case 12: c.get<uint64_t>(); break;
@@ -123,13 +129,17 @@ extern "C" int32_t lle_model_load_gguf(const char* path, lle_model** out) {
     return fail(LLE_EIO, "gguf: stat failed");
   }
   const size_t size = (size_t)st.st_size;
-  void* map = size ? mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0) : MAP_FAILED;
+  // an empty file maps nothing and fails the magic check like any other short file
+  static const uint8_t kEmpty[1] = {0};
+  void* map = size ? mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0) : (void*)kEmpty;
   close(fd);
   if (map == MAP_FAILED) return fail(LLE_EIO, "gguf: mmap failed");
   struct Unmap {
     void* p;
     size_t n;
-    ~Unmap() { munmap(p, n); }
+    ~Unmap() {
+      if (n) munmap(p, n);
+    }
   } unmap{map, size};
 
   Cursor c{(const uint8_t*)map, (const uint8_t*)map + size};
@@ -186,31 +196,45 @@ extern "C" int32_t lle_model_load_gguf(const char* path, lle_model** out) {
   memcpy(&d.ln_eps_bits, &eps, 4);
   memcpy(&d.rope_base_bits, &base, 4);
   if (d.n_layer == 0 || d.d_model == 0) return fail(LLE_EINVAL, "embed: missing model params in GGUF metadata");
-  if (d.n_layer > 4096) return fail(LLE_EINVAL, "embed: implausible block_count");
+  if (d.n_layer < 0 || d.n_layer > 4096) return fail(LLE_EINVAL, "embed: implausible block_count");
 
+  // The first failing tensor (in LoadBertModel's order) decides the error: a missing name is
+  // ENOTFOUND (loadTensor's "tensor %q not found", bert.go:132-136); dims whose element count,
+  // row count or byte size overflow, or data outside the file (the reference's mmap slice
+  // would panic, bert.go:137-139), are EIO.
   std::string missing;
+  int missing_code = LLE_OK;
   auto tensor = [&](const std::string& name) -> lle_tensor {
     lle_tensor t;
     memset(&t, 0, sizeof(t));
+    auto bad = [&](int code, const std::string& msg) {
+      if (missing_code == LLE_OK) {
+        missing_code = code;
+        missing = msg;
+      }
+      return t;
+    };
     auto it = tensors.find(name);
-    if (it == tensors.end()) {
-      if (missing.empty()) missing = name;
-      return t;
-    }
+    if (it == tensors.end()) return bad(LLE_ENOTFOUND, "tensor \"" + name + "\" not found");
     const TInfo& ti = it->second;
+    // NumElements / ByteSize (reader.go:185-204) in checked arithmetic
     uint64_t nel = 1;
-    for (uint64_t x : ti.dims) nel *= x;
-    uint64_t bs = 0, ts = 0;
-    const uint64_t bytes = block_geometry(ti.type, &bs, &ts) ? (nel / bs) * ts : 0;
-    const uint64_t off = data_off + ti.offset;
-    if (off > size || bytes > size - off) {
-      if (missing.empty()) missing = name + " (data past end of file)";
-      return t;
-    }
+    for (uint64_t x : ti.dims)
+      if (__builtin_mul_overflow(nel, x, &nel)) return bad(LLE_EIO, "gguf: tensor " + name + ": element count overflows");
+    uint64_t bs = 0, ts = 0, bytes = 0;
+    if (block_geometry(ti.type, &bs, &ts) && __builtin_mul_overflow(nel / bs, ts, &bytes))
+      return bad(LLE_EIO, "gguf: tensor " + name + ": byte size overflows");
+    uint64_t off = 0;
+    if (__builtin_add_overflow(data_off, ti.offset, &off) || off > size || bytes > size - off)
+      return bad(LLE_EIO, "gguf: tensor " + name + ": data past end of file");
+    uint64_t ne1 = 1;
+    for (size_t k = 1; k < ti.dims.size(); k++) ne1 *= ti.dims[k];  // <= nel: cannot overflow
+    const uint64_t ne0 = ti.dims.empty() ? 0 : ti.dims[0];
+    if (ne0 > (uint64_t)INT32_MAX || ne1 > (uint64_t)INT32_MAX)
+      return bad(LLE_EIO, "gguf: tensor " + name + ": a dimension above 2^31-1");
     t.type = (int32_t)ti.type;
-    t.ne0 = ti.dims.empty() ? 0 : (int64_t)ti.dims[0];
-    t.ne1 = 1;
-    for (size_t k = 1; k < ti.dims.size(); k++) t.ne1 *= (int64_t)ti.dims[k];
+    t.ne0 = (int64_t)ne0;
+    t.ne1 = (int64_t)ne1;
     t.data = (const uint8_t*)map + off;
     t.nbytes = (int64_t)bytes;
     return t;
@@ -233,7 +257,7 @@ extern "C" int32_t lle_model_load_gguf(const char* path, lle_model** out) {
     onw[l] = tensor(p + "layer_output_norm.weight");
     onb[l] = tensor(p + "layer_output_norm.bias");
   }
-  if (!missing.empty()) return fail(LLE_ENOTFOUND, "tensor \"" + missing + "\" not found");
+  if (missing_code != LLE_OK) return fail(missing_code, missing);
   d.qkv = qkv.data();
   d.out = o.data();
   d.attn_norm_w = anw.data();

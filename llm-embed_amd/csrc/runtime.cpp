@@ -91,16 +91,22 @@ struct lle_model {
   int32_t *ids = nullptr, *mask = nullptr, *status = nullptr;
   int32_t *tokrow = nullptr, *seq_off = nullptr;  // packed-row tables of host-pointer batches
   float* out = nullptr;
-  // HIP graphs of small forwards, keyed by shape, rows, pointers and stream
+  // HIP graphs of small forwards, keyed by shape, rows, pointers and stream. A key is captured
+  // the second time it runs (a one-off shape, e.g. one text's length, stays eager) and entries
+  // are evicted least recently used first.
   struct GraphEntry {
     int B, L, T, out_dim;
     const void *ids, *mask;
     void* out;
     hipStream_t st;
-    hipGraphExec_t exec;
+    hipGraphExec_t exec;  // null: seen once, not captured yet
+    uint64_t last_use;
   };
   std::vector<GraphEntry> graphs;
+  uint64_t graph_tick = 0;
   bool use_graphs = true;
+  // joins a caller's stream to the model's stream (forwards always run on the latter)
+  hipEvent_t ev_in = nullptr, ev_out = nullptr;
   // timing
   bool timing = false;
   std::string timing_only;  // non-empty: only this kernel class is bracketed, read at get_timing
@@ -120,7 +126,8 @@ static int dev_alloc(lle_model* m, void** p, size_t bytes) {
 }
 
 static void clear_graphs(lle_model* m) {
-  for (auto& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
+  for (auto& g : m->graphs)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
   m->graphs.clear();
 }
 
@@ -410,44 +417,84 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
   return LLE_OK;
 }
 
-// Forwards of up to this many tokens are captured once into a HIP graph and replayed: they are
-// launch-bound (~90 kernels), and a replay removes the per-kernel host launch cost.
+// Forwards of up to this many tokens are captured into a HIP graph and replayed: they are
+// launch-bound (~60 kernels), and a replay removes the per-kernel host launch cost.
 constexpr int64_t GRAPH_MAX_TOKENS = 4096;
-constexpr size_t GRAPH_CACHE = 32;
+constexpr size_t GRAPH_EXECS = 32;  // captured graphs kept per model
+constexpr size_t GRAPH_KEYS = 128;  // keys remembered (captured or seen once)
 
 static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim,
                        float* d_out, hipStream_t st, const Packing* pk = nullptr) {
   const int T = pk ? pk->T : B * L;
-  if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS)
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  // a stream the caller is capturing already records this forward into the caller's graph
+  if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS ||
+      hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
     return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+  const uint64_t now = ++m->graph_tick;
+  lle_model::GraphEntry* e = nullptr;
   for (auto& g : m->graphs)
     if (g.B == B && g.L == L && g.T == T && g.out_dim == out_dim && g.ids == d_ids && g.mask == d_mask &&
         g.out == d_out && g.st == st) {
-      LLE_HIP(hipGraphLaunch(g.exec, st));
-      return LLE_OK;
+      e = &g;
+      break;
     }
+  if (e && e->exec) {
+    e->last_use = now;
+    LLE_HIP(hipGraphLaunch(e->exec, st));
+    return LLE_OK;
+  }
+  if (!e) {  // first sighting: run eagerly, remember the key
+    if (m->graphs.size() >= GRAPH_KEYS) {
+      auto lru = std::min_element(m->graphs.begin(), m->graphs.end(),
+                                  [](const lle_model::GraphEntry& a, const lle_model::GraphEntry& b) { return a.last_use < b.last_use; });
+      if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
+      m->graphs.erase(lru);
+    }
+    m->graphs.push_back({B, L, T, out_dim, d_ids, d_mask, d_out, st, nullptr, now});
+    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+  }
+  // second sighting: capture, keeping at most GRAPH_EXECS instantiated graphs
+  e->last_use = now;
+  const size_t idx = (size_t)(e - m->graphs.data());
+  size_t n_exec = 0;
+  for (auto& g : m->graphs) n_exec += g.exec != nullptr;
+  if (n_exec >= GRAPH_EXECS) {
+    lle_model::GraphEntry* lru = nullptr;
+    for (auto& g : m->graphs)
+      if (g.exec && (!lru || g.last_use < lru->last_use)) lru = &g;
+    (void)hipGraphExecDestroy(lru->exec);
+    lru->exec = nullptr;
+  }
   hipGraph_t graph = nullptr;
-  LLE_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    (void)hipGetLastError();
+    m->use_graphs = false;  // capture unsupported here: eager from now on
+    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+  }
   const int rc = forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
-  const hipError_t e = hipStreamEndCapture(st, &graph);
+  const hipError_t ce = hipStreamEndCapture(st, &graph);
+  if (rc != LLE_OK) {  // a failing forward is reported; it does not turn graphs off
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    return rc;
+  }
   hipGraphExec_t exec = nullptr;
-  if (rc == LLE_OK && e == hipSuccess && graph &&
-      hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess) {
+  if (ce == hipSuccess && graph && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess) {
     (void)hipGraphDestroy(graph);
-    if (m->graphs.size() >= GRAPH_CACHE) {
-      (void)hipGraphExecDestroy(m->graphs.front().exec);
-      m->graphs.erase(m->graphs.begin());
-    }
-    m->graphs.push_back({B, L, T, out_dim, d_ids, d_mask, d_out, st, exec});
+    m->graphs[idx].exec = exec;
     LLE_HIP(hipGraphLaunch(exec, st));
     return LLE_OK;
   }
-  // capture unavailable: run eagerly from now on
   if (graph) (void)hipGraphDestroy(graph);
   (void)hipGetLastError();
   m->use_graphs = false;
   return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
 }
+
+static int64_t heads_bytes(const lle_model* m, int64_t B, int64_t L) { return B * m->H * ((L + 63) / 64 * 64) * 64 * 2; }
+// The attention grid's z dimension is the sequence index.
+constexpr int kMaxBatch = 65535;
 
 static int check_batch(lle_model* m, int B, int L) {
   if (!m) return fail(LLE_EINVAL, "null model");
@@ -457,6 +504,11 @@ static int check_batch(lle_model* m, int B, int L) {
   // the GEMMs address X ([B*L][d_ff] f16 at most) with 32-bit buffer offsets
   if ((int64_t)B * L * std::max(m->F, m->D) * 2 > INT32_MAX)
     return fail(LLE_EINVAL, "batch too large: B*L*d_ff*2 bytes must stay below 2^31");
+  // so do the QKV epilogue and the attention on the head buffers [B][H][Lp][64] f16, whose
+  // rows are padded to Lp = L rounded up to 64 (up to 64 / L times the token count)
+  if (heads_bytes(m, B, L) > INT32_MAX)
+    return fail(LLE_EINVAL, "batch too large: B*n_head*Lp*64*2 bytes (Lp = L rounded up to 64) must stay below 2^31");
+  if (B > kMaxBatch) return fail(LLE_EINVAL, "batch too large: more than 65535 sequences (attention grid)");
   if (L > 8192) return fail(LLE_EUNSUPPORTED, "sequence length above 8192 (the pooling kernel's row list)");
   return LLE_OK;
 }
@@ -589,7 +641,8 @@ static int check_tensor(const lle_tensor& t, const char* name, int64_t ne0, int6
                                 "], expected [" + std::to_string(ne0) + ", " + std::to_string(ne1) + "]");
   const int64_t rb = row_bytes(t.type, t.ne0);
   if (rb < 0) return fail(LLE_EUNSUPPORTED, std::string(name) + ": unsupported ggml type " + std::to_string(t.type));
-  if (t.nbytes < rb * std::max<int64_t>(t.ne1, 1))
+  int64_t need = 0;
+  if (t.ne1 < 0 || __builtin_mul_overflow(rb, std::max<int64_t>(t.ne1, 1), &need) || t.nbytes < need)
     return fail(LLE_EINVAL, std::string(name) + ": data shorter than its ByteSize");
   return LLE_OK;
 }
@@ -623,14 +676,17 @@ static void destroy_model(lle_model* m) {
   }
   for (auto e : m->event_pool) (void)hipEventDestroy(e);
   if (m->status) (void)hipFree(m->status);
+  if (m->ev_in) (void)hipEventDestroy(m->ev_in);
+  if (m->ev_out) (void)hipEventDestroy(m->ev_out);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
 }
 
 static int create_model(const lle_model_desc* d, lle_model** out) {
   if (!d || !out) return fail(LLE_EINVAL, "null argument");
-  int rc = ensure_init();
-  if (rc) return rc;
+  // the description is validated before the device is touched: a malformed model fails the
+  // same way with or without a GPU
+  int rc = LLE_OK;
   if (d->n_layer <= 0 || d->d_model <= 0) return fail(LLE_EINVAL, "embed: missing model params in GGUF metadata");
   if (d->n_head <= 0 || d->d_model % d->n_head != 0 || d->d_model / d->n_head != 64)
     return fail(LLE_EUNSUPPORTED, "head_dim must be 64 (d_model=" + std::to_string(d->d_model) + ", heads=" +
@@ -666,6 +722,9 @@ static int create_model(const lle_model_desc* d, lle_model** out) {
     if (tu != tg)
       return fail(LLE_EUNSUPPORTED, p + "ffn_up and ffn_gate have different ggml types; the fused up||gate GEMM needs one");
   }
+  if (d->token_embd.ne1 <= 0 || d->token_embd.ne1 > INT32_MAX)
+    return fail(LLE_EINVAL, "token_embd.weight: vocabulary size must be in [1, 2^31)");
+  if ((rc = ensure_init())) return rc;
 
   lle_model* m = new lle_model();
   m->device = g_device;
@@ -683,6 +742,9 @@ static int create_model(const lle_model_desc* d, lle_model** out) {
   };
   if (hipSetDevice(m->device) != hipSuccess) return bail(fail(LLE_EDEVICE, "hipSetDevice failed"));
   if (hipStreamCreate(&m->stream) != hipSuccess) return bail(fail(LLE_EDEVICE, "hipStreamCreate failed"));
+  if (hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming) != hipSuccess)
+    return bail(fail(LLE_EDEVICE, "hipEventCreate failed"));
   if (hipMalloc((void**)&m->status, 4) != hipSuccess) return bail(fail(LLE_ENOMEM, "hipMalloc status"));
   (void)hipMemset(m->status, 0, 4);
 
@@ -797,7 +859,7 @@ int32_t lle_info(char* buf, int32_t cap) {
   } else {
     s += " device=uninitialised";
   }
-  s += " gemm=mfma_f32_16x16x32_f16(dequant->f16 in LDS, f32 accumulate, 256-wide K chunks)";
+  s += " gemm=mfma_f32_16x16x32_f16(dequant->f16 in LDS, f32 accumulate, canonical K chunks of 768 (256 when K % 768 != 0))";
   s += " attention=mfma flash (online max, exact x<-10 cutoff)";
   snprintf(buf, (size_t)cap, "%s", s.c_str());
   return (int32_t)std::min<size_t>(s.size(), (size_t)cap - 1);
@@ -907,7 +969,8 @@ int32_t lle_embed_texts(lle_model* m, const lle_tokenizer* t, const char* const*
     // its padded [B][L] tables stay within 4 x budget (buffers, 32-bit offsets)
     int32_t j = i + 1;
     int64_t valid = L;
-    while (j < n && valid + (int64_t)v[order[j]].size() <= cap && (int64_t)(j - i + 1) * L <= 4 * cap) {
+    while (j < n && valid + (int64_t)v[order[j]].size() <= cap && (int64_t)(j - i + 1) * L <= 4 * cap &&
+           j - i + 1 <= kMaxBatch && heads_bytes(m, j - i + 1, L) <= INT32_MAX) {
       valid += (int64_t)v[order[j]].size();
       j++;
     }
@@ -933,6 +996,23 @@ int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask
   return run_host(m, ids, mask, B, L, m ? m->D : 0, nullptr, hidden);
 }
 
+// Async forwards run on the model's stream whatever stream the caller passes: the workspace is
+// the model's, so two calls must not overlap on the device. The caller's stream is joined by
+// events: the model's stream first waits for the caller's earlier work, and the caller's stream
+// then waits for the forward.
+static int join_in(lle_model* m, hipStream_t cs) {
+  if (cs == m->stream) return LLE_OK;
+  LLE_HIP(hipEventRecord(m->ev_in, cs));
+  LLE_HIP(hipStreamWaitEvent(m->stream, m->ev_in, 0));
+  return LLE_OK;
+}
+static int join_out(lle_model* m, hipStream_t cs) {
+  if (cs == m->stream) return LLE_OK;
+  LLE_HIP(hipEventRecord(m->ev_out, m->stream));
+  LLE_HIP(hipStreamWaitEvent(cs, m->ev_out, 0));
+  return LLE_OK;
+}
+
 int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int32_t B, int32_t L,
                               int32_t out_dim, float* d_out, void* stream) {
   int rc = check_batch(m, B, L);
@@ -942,8 +1022,10 @@ int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t*
   std::lock_guard<std::mutex> lk(m->mu);
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L))) return rc;
-  hipStream_t st = stream ? (hipStream_t)stream : m->stream;
+  const hipStream_t cs = stream ? (hipStream_t)stream : m->stream, st = m->stream;
+  if ((rc = join_in(m, cs))) return rc;
   if ((rc = run_forward(m, d_ids, d_mask, B, L, out_dim, d_out, st))) return rc;
+  if ((rc = join_out(m, cs))) return rc;
   if (m->timing && m->timing_only.empty()) {
     LLE_HIP(hipStreamSynchronize(st));
     collect_timing(m);
@@ -961,10 +1043,12 @@ int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t
   std::lock_guard<std::mutex> lk(m->mu);
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L, T))) return rc;
-  hipStream_t st = stream ? (hipStream_t)stream : m->stream;
+  const hipStream_t cs = stream ? (hipStream_t)stream : m->stream, st = m->stream;
+  if ((rc = join_in(m, cs))) return rc;
   LAUNCH(launch_pack_tables(d_seq_off, B, T, L, m->seq_off, m->tokrow, m->mask, m->status, st));
   Packing pk{T, m->tokrow, m->seq_off};
   if ((rc = run_forward(m, d_ids, m->mask, B, L, out_dim, d_out, st, &pk))) return rc;
+  if ((rc = join_out(m, cs))) return rc;
   if (m->timing && m->timing_only.empty()) {
     LLE_HIP(hipStreamSynchronize(st));
     collect_timing(m);
