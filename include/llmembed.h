@@ -150,6 +150,20 @@ int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask
 int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t* d_seq_off, int32_t B, int32_t T,
                                int32_t L, int32_t out_dim, float* d_out, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): lle_embed_packed_async's forward
+ * (same arguments, same rows bit for bit) with every activation buffer in one fixed device array
+ * of LLE_NOALLOC_SCRATCH_BYTES per device (set up by lle_init, held until the process ends),
+ * so the call makes no device allocation. It runs eagerly on `stream` itself (NULL = the
+ * model's stream), with no graph capture of its own and no timing events, so a caller may
+ * capture it into its own graph. A batch whose activations do not fit is rejected with
+ * LLE_EINVAL and a message giving the bytes it needs (for nomic-bert-base every batch of up to 512
+ * tokens with B x (L rounded up to 64) <= 2048 fits). Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU race: serialise them (one stream, or wait for one before the next). */
+#define LLE_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
+int32_t lle_embed_packed_noalloc(lle_model* m, const int32_t* d_ids, const int32_t* d_seq_off, int32_t B, int32_t T,
+                                 int32_t L, int32_t out_dim, float* d_out, void* stream);
+
 /* Device-side status word of async forwards since the last host-pointer call (bits OR-ed):
  * 1 = a token id was out of range (clamped), 2 = a packed batch's offsets were inconsistent. */
 int32_t lle_model_status(lle_model* m, int32_t* status);

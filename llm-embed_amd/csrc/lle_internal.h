@@ -155,4 +155,16 @@ hipError_t launch_reduce_ln_pool(const float* part, int nch, int M, const float*
 hipError_t launch_pack_tables(const int32_t* in_off, int B, int T, int L, int32_t* off, int32_t* tokrow,
                               int32_t* mask, int32_t* status, hipStream_t st);
 
+// ---------------------------------------------------------------------------------------
+// No-allocation packed forward (lle_embed_packed_noalloc, noalloc.hip).
+// Resolves the device address of the fixed scratch array on `device` (which must be current);
+// once per device, thread-safe. Called by lle_init.
+int noalloc_setup(int device);
+int model_device(const lle_model* m);
+// lle_embed_packed_async's forward with every activation buffer carved from `scratch`
+// (scratch_bytes long) instead of the model's workspace; enqueued eagerly on `stream` (NULL: the
+// model's stream), no graph capture, no timing events, no allocation.
+int embed_packed_scratch(lle_model* m, const int32_t* d_ids, const int32_t* d_seq_off, int B, int T, int L,
+                         int out_dim, float* d_out, hipStream_t stream, void* scratch, size_t scratch_bytes);
+
 }  // namespace lle

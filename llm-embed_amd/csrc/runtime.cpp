@@ -59,6 +59,19 @@ struct Layer {
   float *anw = nullptr, *anb = nullptr, *onw = nullptr, *onb = nullptr;
 };
 
+// Activation buffers of one forward (device pointers). The model owns a grow-only set; the
+// no-allocation entry carves one out of a fixed device array instead.
+struct Workspace {
+  float* h = nullptr;   // residual stream f32 [rows][D]
+  float* h2 = nullptr;  // second residual buffer of the small-batch schedule [16][D]
+  __half* h16 = nullptr;  // f16 copy of h (GEMM input)
+  __half *q = nullptr, *k = nullptr, *vt = nullptr;  // [B][H][Lp][64] / [B][H][64][Lp]
+  __half *attn = nullptr, *ff = nullptr;             // [rows][D], [rows][F]
+  float* part = nullptr;                             // split-K partials below 1024 rows
+  int32_t *ids = nullptr, *mask = nullptr, *tokrow = nullptr, *seq_off = nullptr;
+  float* out = nullptr;  // [B][D] embeddings of host-pointer calls
+};
+
 }  // namespace lle
 
 struct lle_weight {
@@ -80,17 +93,11 @@ struct lle_model {
   std::vector<void*> allocs;
   hipStream_t stream = nullptr;
   std::mutex mu;
-  // workspace
+  // workspace (grow-only)
   size_t ws_T = 0, ws_heads = 0, ws_part = 0;
   int ws_B = 0;
-  float* h = nullptr;
-  float* h2 = nullptr;  // second residual buffer of the fused small-batch layer schedule (16 x D)
-  __half* h16 = nullptr;
-  __half *q = nullptr, *k = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
-  float* part = nullptr;
-  int32_t *ids = nullptr, *mask = nullptr, *status = nullptr;
-  int32_t *tokrow = nullptr, *seq_off = nullptr;  // packed-row tables of host-pointer batches
-  float* out = nullptr;
+  lle::Workspace ws;
+  int32_t* status = nullptr;  // device status word of async forwards (bits, see lle_model_status)
   // HIP graphs of small forwards, keyed by shape, rows, pointers and stream. A key is captured
   // the second time it runs (a one-off shape, e.g. one text's length, stays eager) and entries
   // are evicted least recently used first.
@@ -133,11 +140,11 @@ static void clear_graphs(lle_model* m) {
 
 static void ws_free(lle_model* m) {
   clear_graphs(m);
-  void* bufs[] = {m->h, m->h2, m->h16, m->q, m->k, m->vt, m->attn, m->ff, m->part, m->ids, m->mask, m->tokrow, m->seq_off, m->out};
+  Workspace& w = m->ws;
+  void* bufs[] = {w.h, w.h2, w.h16, w.q, w.k, w.vt, w.attn, w.ff, w.part, w.ids, w.mask, w.tokrow, w.seq_off, w.out};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
-  m->h = nullptr; m->h2 = nullptr; m->h16 = nullptr; m->q = m->k = m->vt = m->attn = m->ff = nullptr;
-  m->part = nullptr; m->ids = m->mask = m->tokrow = m->seq_off = nullptr; m->out = nullptr;
+  w = Workspace{};
   m->ws_T = m->ws_heads = m->ws_part = 0;
   m->ws_B = 0;
 }
@@ -169,20 +176,21 @@ static int ensure_ws(lle_model* m, int B, int L, int64_t rows = -1) {
   const int nB = std::max(B, m->ws_B);
   LLE_HIP(hipStreamSynchronize(m->stream));
   ws_free(m);
-  WS_ALLOC(m->h, nT * m->D * 4);
-  WS_ALLOC(m->h2, (size_t)16 * m->D * 4);
-  WS_ALLOC(m->h16, nT * m->D * 2);
-  WS_ALLOC(m->q, nH * 2);
-  WS_ALLOC(m->k, nH * 2);
-  WS_ALLOC(m->vt, nH * 2);
-  WS_ALLOC(m->attn, nT * m->D * 2);
-  WS_ALLOC(m->ff, nT * m->F * 2);
-  if (nP) WS_ALLOC(m->part, nP * 4);
-  WS_ALLOC(m->ids, nT * 4);
-  WS_ALLOC(m->mask, nT * 4);
-  WS_ALLOC(m->tokrow, nT * 4);
-  WS_ALLOC(m->seq_off, ((size_t)nB + 1) * 4);
-  WS_ALLOC(m->out, (size_t)nB * m->D * 4);
+  Workspace& w = m->ws;
+  WS_ALLOC(w.h, nT * m->D * 4);
+  WS_ALLOC(w.h2, (size_t)16 * m->D * 4);
+  WS_ALLOC(w.h16, nT * m->D * 2);
+  WS_ALLOC(w.q, nH * 2);
+  WS_ALLOC(w.k, nH * 2);
+  WS_ALLOC(w.vt, nH * 2);
+  WS_ALLOC(w.attn, nT * m->D * 2);
+  WS_ALLOC(w.ff, nT * m->F * 2);
+  if (nP) WS_ALLOC(w.part, nP * 4);
+  WS_ALLOC(w.ids, nT * 4);
+  WS_ALLOC(w.mask, nT * 4);
+  WS_ALLOC(w.tokrow, nT * 4);
+  WS_ALLOC(w.seq_off, ((size_t)nB + 1) * 4);
+  WS_ALLOC(w.out, (size_t)nB * m->D * 4);
   m->ws_T = nT;
   m->ws_heads = nH;
   m->ws_part = nP;
@@ -208,8 +216,8 @@ struct Scope {
   hipStream_t st;
   Timer t;
   bool on;
-  Scope(lle_model* m_, hipStream_t st_, const char* name, double flops, double bytes)
-      : m(m_), st(st_), on(m_->timing && (m_->timing_only.empty() || m_->timing_only == name)) {
+  Scope(lle_model* m_, hipStream_t st_, const char* name, double flops, double bytes, bool allowed = true)
+      : m(m_), st(st_), on(allowed && m_->timing && (m_->timing_only.empty() || m_->timing_only == name)) {
     if (on) {
       t.name = name;
       t.flops = flops;
@@ -277,18 +285,19 @@ struct Packing {
   const int32_t* seq_off;
 };
 
-// ids / mask / out are device pointers already placed in m's workspace or the caller's; with
-// `pk`, ids are the packed rows' ids and the mask stays [B][L].
-static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim, float* d_out,
-                   hipStream_t st, const Packing* pk = nullptr) {
+// ids / mask / out are device pointers already placed in a workspace or the caller's; with
+// `pk`, ids are the packed rows' ids and the mask stays [B][L]. The activations live in `w`;
+// `timed` = false keeps the launches free of timing events (no host-side event creation).
+static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const int32_t* d_mask, int B, int L,
+                   int out_dim, float* d_out, hipStream_t st, const Packing* pk = nullptr, bool timed = true) {
   const int D = m->D, H = m->H, F = m->F;
   const int T = pk ? pk->T : B * L, Lp = (L + 63) / 64 * 64;
   const int32_t* tokrow = pk ? pk->tokrow : nullptr;
   const int32_t* seq_off = pk ? pk->seq_off : nullptr;
   {
     EmbedArgs a{d_ids, T, m->vocab, m->tok_type, m->tok, m->tok_row_bytes, m->type0, m->enw, m->enb, m->eps, D,
-                m->h, m->h16, m->status};
-    Scope s(m, st, "embed_ln", 0, (double)T * (m->tok_row_bytes + D * 6));
+                w.h, w.h16, m->status};
+    Scope s(m, st, "embed_ln", 0, (double)T * (m->tok_row_bytes + D * 6), timed);
     LAUNCH(launch_embed_ln(a, st));
   }
   // Batches of <= 16 tokens: each LayerNorm runs inside the GEMM that consumes it (every block
@@ -307,58 +316,58 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
       g.Lp = Lp;
       g.n_head = H;
       g.d_model = D;
-      g.part = m->part;
+      g.part = w.part;
       g.tokrow = tokrow;
       {
         g.w = &ly.qkv;
-        g.x = m->h16;
-        g.q = m->q;
-        g.k = m->k;
-        g.vt = m->vt;
-        Scope s(m, st, "gemm_qkv", 2.0 * T * ly.qkv.N * ly.qkv.K, wbytes(ly.qkv) + (double)T * (D * 2 + 3 * D * 2));
+        g.x = w.h16;
+        g.q = w.q;
+        g.k = w.k;
+        g.vt = w.vt;
+        Scope s(m, st, "gemm_qkv", 2.0 * T * ly.qkv.N * ly.qkv.K, wbytes(ly.qkv) + (double)T * (D * 2 + 3 * D * 2), timed);
         if (l == 0) {
           LAUNCH(launch_gemm(g, EPI_QKV, st));
         } else {
           const Layer& pv = m->layers[l - 1];
-          const LnPrologue ln{m->h2, m->part, 4, pv.onw, pv.onb, m->eps, m->h};
+          const LnPrologue ln{w.h2, w.part, 4, pv.onw, pv.onb, m->eps, w.h};
           LAUNCH(launch_gemm_lnx(g, EPI_QKV, ln, st));
         }
       }
       {
-        AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D, seq_off};
-        Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
+        AttnArgs a{w.q, w.k, w.vt, d_mask, w.attn, B, L, Lp, H, D, seq_off};
+        Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4, timed);
         LAUNCH(launch_attention(a, st));
       }
       {
         g.w = &ly.out;
-        g.x = m->attn;
-        g.y = m->h;
-        Scope s(m, st, "gemm_out_ln", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 8));
+        g.x = w.attn;
+        g.y = w.h;
+        Scope s(m, st, "gemm_out_ln", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 8), timed);
         LAUNCH(launch_gemm(g, EPI_RESID, st));
       }
       {
         g.w = &ly.upgate;
-        g.g = m->ff;
-        const LnPrologue ln{m->h, nullptr, 0, ly.anw, ly.anb, m->eps, m->h2};
-        Scope s(m, st, "gemm_upgate", 2.0 * T * ly.upgate.N * ly.upgate.K, wbytes(ly.upgate) + (double)T * (D * 4 + F * 2));
+        g.g = w.ff;
+        const LnPrologue ln{w.h, nullptr, 0, ly.anw, ly.anb, m->eps, w.h2};
+        Scope s(m, st, "gemm_upgate", 2.0 * T * ly.upgate.N * ly.upgate.K, wbytes(ly.upgate) + (double)T * (D * 4 + F * 2), timed);
         LAUNCH(launch_gemm_lnx(g, EPI_GEGLU, ln, st));
       }
       {
         g.w = &ly.down;
-        g.x = m->ff;
-        g.y = m->h2;
-        Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 16));
+        g.x = w.ff;
+        g.y = w.h2;
+        Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 16), timed);
         LAUNCH(launch_gemm_partials(g, st));
       }
     }
     const Layer& last = m->layers[m->n_layer - 1];
     if (d_out) {  // the last LayerNorm's rows only feed the pool: one kernel, rows kept in LDS
-      Scope s(m, st, "pool", 0, (double)T * D * 24);
-      LAUNCH(launch_reduce_ln_pool(m->part, 4, T, m->h2, last.onw, last.onb, m->eps, d_mask, seq_off, B, L, D,
+      Scope s(m, st, "pool", 0, (double)T * D * 24, timed);
+      LAUNCH(launch_reduce_ln_pool(w.part, 4, T, w.h2, last.onw, last.onb, m->eps, d_mask, seq_off, B, L, D,
                                    out_dim, d_out, st));
     } else {
-      Scope s(m, st, "ln", 0, (double)T * D * 26);
-      LAUNCH(launch_reduce_resid_ln(m->part, 4, T, D, m->h2, m->h, m->h16, last.onw, last.onb, m->eps, st));
+      Scope s(m, st, "ln", 0, (double)T * D * 26, timed);
+      LAUNCH(launch_reduce_resid_ln(w.part, 4, T, D, w.h2, w.h, w.h16, last.onw, last.onb, m->eps, st));
     }
     return LLE_OK;
   }
@@ -372,47 +381,47 @@ static int forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, in
     g.Lp = Lp;
     g.n_head = H;
     g.d_model = D;
-    g.part = m->part;
+    g.part = w.part;
     g.tokrow = tokrow;
     {
       g.w = &ly.qkv;
-      g.x = m->h16;
-      g.q = m->q;
-      g.k = m->k;
-      g.vt = m->vt;
-      Scope s(m, st, "gemm_qkv", 2.0 * T * ly.qkv.N * ly.qkv.K, wbytes(ly.qkv) + (double)T * (D * 2 + 3 * D * 2));
+      g.x = w.h16;
+      g.q = w.q;
+      g.k = w.k;
+      g.vt = w.vt;
+      Scope s(m, st, "gemm_qkv", 2.0 * T * ly.qkv.N * ly.qkv.K, wbytes(ly.qkv) + (double)T * (D * 2 + 3 * D * 2), timed);
       LAUNCH(launch_gemm(g, EPI_QKV, st));
     }
     {
-      AttnArgs a{m->q, m->k, m->vt, d_mask, m->attn, B, L, Lp, H, D, seq_off};
-      Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4);
+      AttnArgs a{w.q, w.k, w.vt, d_mask, w.attn, B, L, Lp, H, D, seq_off};
+      Scope s(m, st, "attention", 4.0 * B * (double)L * L * D, (double)T * D * 2 * 4, timed);
       LAUNCH(launch_attention(a, st));
     }
     {
       g.w = &ly.out;
-      g.x = m->attn;
-      g.y = m->h;
-      Scope s(m, st, "gemm_out_ln", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 18));
-      LAUNCH(launch_gemm_resid_ln(g, ly.anw, ly.anb, m->eps, m->h16, st));
+      g.x = w.attn;
+      g.y = w.h;
+      Scope s(m, st, "gemm_out_ln", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 18), timed);
+      LAUNCH(launch_gemm_resid_ln(g, ly.anw, ly.anb, m->eps, w.h16, st));
     }
     {
       g.w = &ly.upgate;
-      g.x = m->h16;
-      g.g = m->ff;
-      Scope s(m, st, "gemm_upgate", 2.0 * T * ly.upgate.N * ly.upgate.K, wbytes(ly.upgate) + (double)T * (D * 2 + F * 2));
+      g.x = w.h16;
+      g.g = w.ff;
+      Scope s(m, st, "gemm_upgate", 2.0 * T * ly.upgate.N * ly.upgate.K, wbytes(ly.upgate) + (double)T * (D * 2 + F * 2), timed);
       LAUNCH(launch_gemm(g, EPI_GEGLU, st));
     }
     {
       g.w = &ly.down;
-      g.x = m->ff;
-      g.y = m->h;
-      Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 18));
-      LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, m->h16, st));
+      g.x = w.ff;
+      g.y = w.h;
+      Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 18), timed);
+      LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, w.h16, st));
     }
   }
   if (d_out) {
-    Scope s(m, st, "pool", 0, (double)T * D * 4);
-    LAUNCH(launch_pool(m->h, d_mask, seq_off, B, L, D, out_dim, d_out, st));
+    Scope s(m, st, "pool", 0, (double)T * D * 4, timed);
+    LAUNCH(launch_pool(w.h, d_mask, seq_off, B, L, D, out_dim, d_out, st));
   }
   return LLE_OK;
 }
@@ -430,7 +439,7 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
   // a stream the caller is capturing already records this forward into the caller's graph
   if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS ||
       hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
-    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+    return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   const uint64_t now = ++m->graph_tick;
   lle_model::GraphEntry* e = nullptr;
   for (auto& g : m->graphs)
@@ -452,7 +461,7 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
       m->graphs.erase(lru);
     }
     m->graphs.push_back({B, L, T, out_dim, d_ids, d_mask, d_out, st, nullptr, now});
-    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+    return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   }
   // second sighting: capture, keeping at most GRAPH_EXECS instantiated graphs
   e->last_use = now;
@@ -470,9 +479,9 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
   if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
     (void)hipGetLastError();
     m->use_graphs = false;  // capture unsupported here: eager from now on
-    return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+    return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   }
-  const int rc = forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+  const int rc = forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   const hipError_t ce = hipStreamEndCapture(st, &graph);
   if (rc != LLE_OK) {  // a failing forward is reported; it does not turn graphs off
     if (graph) (void)hipGraphDestroy(graph);
@@ -489,7 +498,7 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
   if (graph) (void)hipGraphDestroy(graph);
   (void)hipGetLastError();
   m->use_graphs = false;
-  return forward(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
+  return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
 }
 
 static int64_t heads_bytes(const lle_model* m, int64_t B, int64_t L) { return B * m->H * ((L + 63) / 64 * 64) * 64 * 2; }
@@ -563,21 +572,21 @@ static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L, packed ? (int64_t)pids.size() : -1))) return rc;
   hipStream_t st = m->stream;
-  Packing pk{(int)pids.size(), m->tokrow, m->seq_off};
+  Packing pk{(int)pids.size(), m->ws.tokrow, m->ws.seq_off};
   if (packed) {
-    LLE_HIP(hipMemcpyAsync(m->ids, pids.data(), pids.size() * 4, hipMemcpyHostToDevice, st));
-    LLE_HIP(hipMemcpyAsync(m->tokrow, prow.data(), prow.size() * 4, hipMemcpyHostToDevice, st));
-    LLE_HIP(hipMemcpyAsync(m->seq_off, soff.data(), soff.size() * 4, hipMemcpyHostToDevice, st));
+    LLE_HIP(hipMemcpyAsync(m->ws.ids, pids.data(), pids.size() * 4, hipMemcpyHostToDevice, st));
+    LLE_HIP(hipMemcpyAsync(m->ws.tokrow, prow.data(), prow.size() * 4, hipMemcpyHostToDevice, st));
+    LLE_HIP(hipMemcpyAsync(m->ws.seq_off, soff.data(), soff.size() * 4, hipMemcpyHostToDevice, st));
   } else {
-    LLE_HIP(hipMemcpyAsync(m->ids, ids, T * 4, hipMemcpyHostToDevice, st));
+    LLE_HIP(hipMemcpyAsync(m->ws.ids, ids, T * 4, hipMemcpyHostToDevice, st));
   }
-  LLE_HIP(hipMemcpyAsync(m->mask, mask, T * 4, hipMemcpyHostToDevice, st));
+  LLE_HIP(hipMemcpyAsync(m->ws.mask, mask, T * 4, hipMemcpyHostToDevice, st));
   LLE_HIP(hipMemsetAsync(m->status, 0, 4, st));
-  if ((rc = run_forward(m, m->ids, m->mask, B, L, out_dim, out ? m->out : nullptr, st, packed ? &pk : nullptr)))
+  if ((rc = run_forward(m, m->ws.ids, m->ws.mask, B, L, out_dim, out ? m->ws.out : nullptr, st, packed ? &pk : nullptr)))
     return rc;
   const int od = std::min(out_dim, m->D);
-  if (out) LLE_HIP(hipMemcpyAsync(out, m->out, (size_t)B * od * 4, hipMemcpyDeviceToHost, st));
-  if (hidden) LLE_HIP(hipMemcpyAsync(hidden, m->h, T * m->D * 4, hipMemcpyDeviceToHost, st));
+  if (out) LLE_HIP(hipMemcpyAsync(out, m->ws.out, (size_t)B * od * 4, hipMemcpyDeviceToHost, st));
+  if (hidden) LLE_HIP(hipMemcpyAsync(hidden, m->ws.h, T * m->D * 4, hipMemcpyDeviceToHost, st));
   // host buffers above (pids, prow, soff, ones) must outlive the copies
   LLE_HIP(hipStreamSynchronize(st));
   if (m->timing && m->timing_only.empty()) collect_timing(m);
@@ -821,6 +830,63 @@ static int create_model(const lle_model_desc* d, lle_model** out) {
   return LLE_OK;
 }
 
+// Activations of a packed forward (T rows, B sequences of at most L tokens) laid out from
+// `base`, each buffer 256-byte aligned: the sizes the model's own workspace gives the same call
+// (ensure_ws with T rows). Returns the bytes needed; fills *w when base is non-null.
+static size_t carve_packed(const lle_model* m, int B, int L, int T, uint8_t* base, Workspace* w) {
+  const size_t D = m->D, F = m->F, R = (size_t)T;
+  const size_t heads = (size_t)heads_bytes(m, B, L);
+  auto nch = [](size_t K) { return K % 768 == 0 ? K / 768 : K / 256; };
+  const size_t kd = nch(D), kf = nch(F);
+  const size_t part = R < 1024 ? std::max<size_t>(R, 64) * std::max({kd * 3 * D, kd * 2 * F, kf * D}) * 4 : 0;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base ? base + off : nullptr;
+    off += (std::max<size_t>(bytes, 1) + 255) & ~(size_t)255;
+    return p;
+  };
+  Workspace x;
+  x.h = (float*)take(R * D * 4);
+  x.h2 = (float*)take(16 * D * 4);
+  x.h16 = (__half*)take(R * D * 2);
+  x.q = (__half*)take(heads);
+  x.k = (__half*)take(heads);
+  x.vt = (__half*)take(heads);
+  x.attn = (__half*)take(R * D * 2);
+  x.ff = (__half*)take(R * F * 2);
+  x.part = part ? (float*)take(part) : nullptr;
+  x.mask = (int32_t*)take((size_t)B * L * 4);
+  x.tokrow = (int32_t*)take(R * 4);
+  x.seq_off = (int32_t*)take(((size_t)B + 1) * 4);
+  if (base && w) *w = x;
+  return off;
+}
+
+int model_device(const lle_model* m) { return m ? m->device : -1; }
+
+int embed_packed_scratch(lle_model* m, const int32_t* d_ids, const int32_t* d_seq_off, int B, int T, int L,
+                         int out_dim, float* d_out, hipStream_t stream, void* scratch, size_t scratch_bytes) {
+  int rc = check_batch(m, B, L);
+  if (rc) return rc;
+  if (!d_ids || !d_seq_off || !d_out) return fail(LLE_EINVAL, "null device pointer");
+  if (T < 1 || (int64_t)T > (int64_t)B * L) return fail(LLE_EINVAL, "T must be in [1, B * L]");
+  if (!scratch) return fail(LLE_EDEVICE, "no-allocation scratch not set up on this device");
+  if (out_dim < 1) out_dim = 1;
+  const size_t need = carve_packed(m, B, L, T, nullptr, nullptr);
+  if (need > scratch_bytes)
+    return fail(LLE_EINVAL, "lle_embed_packed_noalloc: this batch needs " + std::to_string(need) +
+                                " bytes of scratch, above the fixed " + std::to_string(scratch_bytes) +
+                                " (fewer tokens or sequences per call)");
+  Workspace w;
+  carve_packed(m, B, L, T, (uint8_t*)scratch, &w);
+  std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  const hipStream_t st = stream ? stream : m->stream;
+  LAUNCH(launch_pack_tables(d_seq_off, B, T, L, w.seq_off, w.tokrow, w.mask, m->status, st));
+  Packing pk{T, w.tokrow, w.seq_off};
+  return forward(m, w, d_ids, w.mask, B, L, out_dim, d_out, st, &pk, /*timed=*/false);
+}
+
 }  // namespace lle
 
 using namespace lle;
@@ -844,6 +910,8 @@ int32_t lle_init(int32_t device) {
     return fail(LLE_EDEVICE, std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950");
   e = hipSetDevice(device);
   if (e != hipSuccess) return fail(LLE_EDEVICE, std::string("hipSetDevice: ") + hipGetErrorString(e));
+  const int rc = noalloc_setup(device);  // the no-allocation entry's device array, with `device` current
+  if (rc) return rc;
   g_device = device;
   return LLE_OK;
 }
@@ -1045,9 +1113,9 @@ int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t
   if ((rc = ensure_ws(m, B, L, T))) return rc;
   const hipStream_t cs = stream ? (hipStream_t)stream : m->stream, st = m->stream;
   if ((rc = join_in(m, cs))) return rc;
-  LAUNCH(launch_pack_tables(d_seq_off, B, T, L, m->seq_off, m->tokrow, m->mask, m->status, st));
-  Packing pk{T, m->tokrow, m->seq_off};
-  if ((rc = run_forward(m, d_ids, m->mask, B, L, out_dim, d_out, st, &pk))) return rc;
+  LAUNCH(launch_pack_tables(d_seq_off, B, T, L, m->ws.seq_off, m->ws.tokrow, m->ws.mask, m->status, st));
+  Packing pk{T, m->ws.tokrow, m->ws.seq_off};
+  if ((rc = run_forward(m, d_ids, m->ws.mask, B, L, out_dim, d_out, st, &pk))) return rc;
   if ((rc = join_out(m, cs))) return rc;
   if (m->timing && m->timing_only.empty()) {
     LLE_HIP(hipStreamSynchronize(st));
