@@ -122,7 +122,8 @@ def main():
         _hip._ok(_hip.rt().hipMemset(src.ptr, 1, n), "hipMemset")
         _hip._ok(_hip.rt().hipMemcpy(dst.ptr, src.ptr, n, _hip.D2D), "hipMemcpy")
         _hip.synchronize()
-        log(f"[bench] traffic probe done: 2 config-{args.probe_config} forwards, 1 copy of 268435456 B")
+        nfw = 60 if args.probe_config == 1 else 2
+        log(f"[bench] traffic probe done: {nfw} config-{args.probe_config} forwards, 1 copy of 268435456 B")
         return
 
     for _ in range(args.warmup):

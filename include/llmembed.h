@@ -168,6 +168,21 @@ int32_t lle_embed_packed_noalloc(lle_model* m, const int32_t* d_ids, const int32
  * 1 = a token id was out of range (clamped), 2 = a packed batch's offsets were inconsistent. */
 int32_t lle_model_status(lle_model* m, int32_t* status);
 
+/* Arithmetic of a model's forwards. LLE_PRECISION_F16 (the default): MFMA GEMMs on f16 operands
+ * (weights rounded once from the exact dequantisation, activations rounded to f16 between
+ * kernels) with f32 accumulation; within the per-vector tolerance of the reference. And
+ * LLE_PRECISION_F32: the reference CPU path's own f32 arithmetic in its order (GemmPrePacked32's
+ * 128-wide K chunks with FMA chains and unfused edge rows, internal/ggml/gemm_avx512.go:67-147;
+ * sequential LayerNorm sums; DotF32 order; exp in f64; internal/embed/bert.go:216-445,
+ * internal/ggml/ops_simd.go, internal/embed/pool.go), on f32 copies of the dequantised weights
+ * made when it is selected (as PreDequant does, bert.go:542-576; 4 bytes per weight), so
+ * embeddings equal the reference's bit for bit up to the last float64 ulp of exp. In F32 mode
+ * lle_embed_batch_async and lle_embed_packed_noalloc return LLE_EUNSUPPORTED (use the host
+ * entries or lle_embed_packed_async, which know each sequence's length). */
+#define LLE_PRECISION_F16 0
+#define LLE_PRECISION_F32 1
+int32_t lle_model_set_precision(lle_model* m, int32_t precision);
+
 /* Kernel timing: enable (1) / disable (0) and read per-kernel-class HIP-event totals.
  * lle_model_set_timing brackets every launch and synchronises at the end of each forward.
  * lle_model_set_timing_kernel brackets only the launches of one kernel class (e.g. "gemm_upgate";

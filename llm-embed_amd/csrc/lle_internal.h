@@ -156,6 +156,39 @@ hipError_t launch_pack_tables(const int32_t* in_off, int B, int T, int L, int32_
                               int32_t* mask, int32_t* status, hipStream_t st);
 
 // ---------------------------------------------------------------------------------------
+// Reference-exact f32 forward (exact.hip): activations f32, weights the f32 dequantisation.
+struct ExactArgs {
+  int T, L, D, H;
+  const int32_t* tokrow;   // packed rows: row t is padded token tokrow[t] = b * L + p (null: t)
+  const int32_t* seq_off;  // packed: [B+1] first row of each sequence (null: rows b*L .. b*L+L-1)
+  const int32_t* mask;     // [B][L]
+  const int32_t* ids;      // embedding: token id of each row
+  int vocab, tok_type;
+  const uint8_t* tok;      // raw GGUF token_embd
+  int64_t tok_row_bytes;
+  const float* type0;      // token_types row 0
+  int32_t* status;
+  const float* lnw;        // LayerNorm weights of the current step
+  const float* lnb;
+  float eps;
+  float* h;                // [T][D] residual stream
+  float *q, *k, *v, *att;  // [T][D]
+  const float* rope_cos;   // [max_seq][32]
+  const float* rope_sin;
+};
+struct ExactGemm {
+  const float* x;  // [T][K]
+  const float* w;  // [N][K]
+  int N, K;
+  float* y;        // EPI_F32: [T][N]; EPI_RESID: [T][N] (+=); EPI_GEGLU: [T][N/2]; EPI_QKV: unused
+};
+hipError_t launch_exact_embed(const ExactArgs& a, hipStream_t st);
+hipError_t launch_exact_ln(const ExactArgs& a, hipStream_t st);
+hipError_t launch_exact_gemm(const ExactArgs& a, const ExactGemm& g, int epi, hipStream_t st);
+hipError_t launch_exact_attention(const ExactArgs& a, hipStream_t st);
+hipError_t launch_exact_pool(const ExactArgs& a, int B, int out_dim, float* out, hipStream_t st);
+
+// ---------------------------------------------------------------------------------------
 // No-allocation packed forward (lle_embed_packed_noalloc, noalloc.hip).
 // Resolves the device address of the fixed scratch array on `device` (which must be current);
 // once per device, thread-safe. Called by lle_init.

@@ -89,6 +89,12 @@ struct lle_model {
   int64_t tok_row_bytes = 0;
   float *type0 = nullptr, *enw = nullptr, *enb = nullptr;
   std::vector<lle::Layer> layers;
+  // LLE_PRECISION_F32: f32 copies of the dequantised projection weights ([N][K] per layer:
+  // qkv, out, up||gate interleaved, down) and the f32 activations of the exact forward
+  int precision = LLE_PRECISION_F16;
+  std::vector<float*> w32;  // 4 per layer
+  size_t ex_T = 0;
+  float *ex_h = nullptr, *ex_q = nullptr, *ex_k = nullptr, *ex_v = nullptr, *ex_att = nullptr, *ex_g = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;
   std::vector<void*> allocs;
   hipStream_t stream = nullptr;
@@ -285,11 +291,114 @@ struct Packing {
   const int32_t* seq_off;
 };
 
+static void ex_free(lle_model* m) {
+  float* bufs[] = {m->ex_h, m->ex_q, m->ex_k, m->ex_v, m->ex_att, m->ex_g};
+  for (float* b : bufs)
+    if (b) (void)hipFree(b);
+  m->ex_h = m->ex_q = m->ex_k = m->ex_v = m->ex_att = m->ex_g = nullptr;
+  m->ex_T = 0;
+}
+
+// f32 activations of the exact forward for `rows` token rows (grow-only).
+static int ensure_exact_ws(lle_model* m, size_t rows) {
+  if (rows <= m->ex_T) return LLE_OK;
+  LLE_HIP(hipStreamSynchronize(m->stream));
+  ex_free(m);
+  const size_t D = m->D, F = m->F;
+  float** dst[] = {&m->ex_h, &m->ex_q, &m->ex_k, &m->ex_v, &m->ex_att, &m->ex_g};
+  const size_t n[] = {rows * D, rows * D, rows * D, rows * D, rows * D, rows * F};
+  for (int i = 0; i < 6; i++) {
+    hipError_t e = hipMalloc((void**)dst[i], std::max<size_t>(n[i], 64) * 4);
+    if (e != hipSuccess) {
+      ex_free(m);
+      return fail(LLE_ENOMEM, std::string("exact workspace hipMalloc: ") + hipGetErrorString(e));
+    }
+  }
+  m->ex_T = rows;
+  return LLE_OK;
+}
+
+// BertModel.Forward in the reference's own f32 arithmetic (exact.hip), for B sequences of
+// length L, or packed rows (pk): sequence b is rows seq_off[b] .. seq_off[b+1]-1 at its own
+// length, as the reference embeds each text at its own length. The residual stream ends in
+// m->ex_h; with d_out, MeanPool + L2Normalize (+ Matryoshka) into d_out.
+static int forward_exact(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim,
+                         float* d_out, hipStream_t st, const Packing* pk) {
+  const int D = m->D, F = m->F, T = pk ? pk->T : B * L;
+  int rc = ensure_exact_ws(m, (size_t)T);
+  if (rc) return rc;
+  ExactArgs a{};
+  a.T = T;
+  a.L = L;
+  a.D = D;
+  a.H = m->H;
+  a.tokrow = pk ? pk->tokrow : nullptr;
+  a.seq_off = pk ? pk->seq_off : nullptr;
+  a.mask = d_mask;
+  a.ids = d_ids;
+  a.vocab = m->vocab;
+  a.tok_type = m->tok_type;
+  a.tok = m->tok;
+  a.tok_row_bytes = m->tok_row_bytes;
+  a.type0 = m->type0;
+  a.status = m->status;
+  a.eps = m->eps;
+  a.h = m->ex_h;
+  a.q = m->ex_q;
+  a.k = m->ex_k;
+  a.v = m->ex_v;
+  a.att = m->ex_att;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  a.lnw = m->enw;
+  a.lnb = m->enb;
+  {
+    Scope s(m, st, "embed_ln", 0, (double)T * (m->tok_row_bytes + D * 8));
+    LAUNCH(launch_exact_embed(a, st));
+  }
+  for (int l = 0; l < m->n_layer; l++) {
+    const Layer& ly = m->layers[l];
+    float* const* w = &m->w32[(size_t)l * 4];
+    {
+      Scope s(m, st, "gemm_qkv", 2.0 * T * 3 * D * D, 3.0 * D * D * 4 + (double)T * D * 16);
+      LAUNCH(launch_exact_gemm(a, ExactGemm{a.h, w[0], 3 * D, D, nullptr}, EPI_QKV, st));
+    }
+    {
+      Scope s(m, st, "attention", 0, (double)T * D * 16);
+      LAUNCH(launch_exact_attention(a, st));
+    }
+    {
+      Scope s(m, st, "gemm_out_ln", 2.0 * T * D * D, (double)D * D * 4 + (double)T * D * 16);
+      LAUNCH(launch_exact_gemm(a, ExactGemm{a.att, w[1], D, D, a.h}, EPI_RESID, st));
+      a.lnw = ly.anw;
+      a.lnb = ly.anb;
+      LAUNCH(launch_exact_ln(a, st));
+    }
+    {
+      Scope s(m, st, "gemm_upgate", 2.0 * T * 2 * F * D, 2.0 * F * D * 4 + (double)T * (D + F) * 4);
+      LAUNCH(launch_exact_gemm(a, ExactGemm{a.h, w[2], 2 * F, D, m->ex_g}, EPI_GEGLU, st));
+    }
+    {
+      Scope s(m, st, "gemm_down_ln", 2.0 * T * D * F, (double)D * F * 4 + (double)T * (F + 3 * D) * 4);
+      LAUNCH(launch_exact_gemm(a, ExactGemm{m->ex_g, w[3], D, F, a.h}, EPI_RESID, st));
+      a.lnw = ly.onw;
+      a.lnb = ly.onb;
+      LAUNCH(launch_exact_ln(a, st));
+    }
+  }
+  if (d_out) {
+    Scope s(m, st, "pool", 0, (double)T * D * 4);
+    LAUNCH(launch_exact_pool(a, B, out_dim, d_out, st));
+  }
+  return LLE_OK;
+}
+
 // ids / mask / out are device pointers already placed in a workspace or the caller's; with
 // `pk`, ids are the packed rows' ids and the mask stays [B][L]. The activations live in `w`;
 // `timed` = false keeps the launches free of timing events (no host-side event creation).
 static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const int32_t* d_mask, int B, int L,
                    int out_dim, float* d_out, hipStream_t st, const Packing* pk = nullptr, bool timed = true) {
+  if (m->precision == LLE_PRECISION_F32) return forward_exact(m, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   const int D = m->D, H = m->H, F = m->F;
   const int T = pk ? pk->T : B * L, Lp = (L + 63) / 64 * 64;
   const int32_t* tokrow = pk ? pk->tokrow : nullptr;
@@ -437,7 +546,7 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
   const int T = pk ? pk->T : B * L;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   // a stream the caller is capturing already records this forward into the caller's graph
-  if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS ||
+  if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS || m->precision != LLE_PRECISION_F16 ||
       hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
     return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   const uint64_t now = ++m->graph_tick;
@@ -586,7 +695,9 @@ static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B
     return rc;
   const int od = std::min(out_dim, m->D);
   if (out) LLE_HIP(hipMemcpyAsync(out, m->ws.out, (size_t)B * od * 4, hipMemcpyDeviceToHost, st));
-  if (hidden) LLE_HIP(hipMemcpyAsync(hidden, m->ws.h, T * m->D * 4, hipMemcpyDeviceToHost, st));
+  if (hidden)
+    LLE_HIP(hipMemcpyAsync(hidden, m->precision == LLE_PRECISION_F32 ? m->ex_h : m->ws.h, T * m->D * 4,
+                           hipMemcpyDeviceToHost, st));
   // host buffers above (pids, prow, soff, ones) must outlive the copies
   LLE_HIP(hipStreamSynchronize(st));
   if (m->timing && m->timing_only.empty()) collect_timing(m);
@@ -678,6 +789,9 @@ static void destroy_model(lle_model* m) {
   (void)hipSetDevice(m->device);
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   ws_free(m);  // also destroys cached graphs
+  ex_free(m);
+  for (float* p : m->w32)
+    if (p) (void)hipFree(p);
   for (void* p : m->allocs) (void)hipFree(p);
   for (auto& t : m->pending) {
     (void)hipEventDestroy(t.a);
@@ -871,6 +985,8 @@ int embed_packed_scratch(lle_model* m, const int32_t* d_ids, const int32_t* d_se
   if (!d_ids || !d_seq_off || !d_out) return fail(LLE_EINVAL, "null device pointer");
   if (T < 1 || (int64_t)T > (int64_t)B * L) return fail(LLE_EINVAL, "T must be in [1, B * L]");
   if (!scratch) return fail(LLE_EDEVICE, "no-allocation scratch not set up on this device");
+  if (m->precision != LLE_PRECISION_F16)
+    return fail(LLE_EUNSUPPORTED, "lle_embed_packed_noalloc runs the f16 forward only (the model is in F32 precision)");
   if (out_dim < 1) out_dim = 1;
   const size_t need = carve_packed(m, B, L, T, nullptr, nullptr);
   if (need > scratch_bytes)
@@ -1088,6 +1204,8 @@ int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t*
   if (!d_ids || !d_mask || !d_out) return fail(LLE_EINVAL, "null device pointer");
   if (out_dim < 1) out_dim = 1;
   std::lock_guard<std::mutex> lk(m->mu);
+  if (m->precision != LLE_PRECISION_F16)
+    return fail(LLE_EUNSUPPORTED, "F32 precision needs each sequence's length: use lle_embed_packed_async or a host entry");
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L))) return rc;
   const hipStream_t cs = stream ? (hipStream_t)stream : m->stream, st = m->stream;
@@ -1130,6 +1248,41 @@ int32_t lle_model_status(lle_model* m, int32_t* status) {
   LLE_HIP(hipSetDevice(m->device));
   LLE_HIP(hipDeviceSynchronize());
   LLE_HIP(hipMemcpy(status, m->status, 4, hipMemcpyDeviceToHost));
+  return LLE_OK;
+}
+
+int32_t lle_model_set_precision(lle_model* m, int32_t precision) {
+  if (!m) return fail(LLE_EINVAL, "null model");
+  if (precision != LLE_PRECISION_F16 && precision != LLE_PRECISION_F32)
+    return fail(LLE_EINVAL, "precision must be LLE_PRECISION_F16 or LLE_PRECISION_F32");
+  std::lock_guard<std::mutex> lk(m->mu);
+  LLE_HIP(hipSetDevice(m->device));
+  LLE_HIP(hipStreamSynchronize(m->stream));
+  if (precision == LLE_PRECISION_F32 && m->w32.empty()) {
+    // PreDequant (internal/embed/bert.go:542-576): every projection dequantised once to f32
+    // [N][K] by the GEMM's own decoder (bit-exact with DequantWeightMatrix)
+    std::vector<float*> w32((size_t)m->n_layer * 4, nullptr);
+    auto undo = [&](int code, const std::string& msg) {
+      for (float* p : w32)
+        if (p) (void)hipFree(p);
+      return fail(code, msg);
+    };
+    for (int l = 0; l < m->n_layer; l++) {
+      const WeightDev* ws[4] = {&m->layers[l].qkv, &m->layers[l].out, &m->layers[l].upgate, &m->layers[l].down};
+      for (int i = 0; i < 4; i++) {
+        float* p = nullptr;
+        hipError_t e = hipMalloc((void**)&p, (size_t)ws[i]->N * ws[i]->K * 4);
+        if (e != hipSuccess) return undo(LLE_ENOMEM, std::string("f32 weight copy hipMalloc: ") + hipGetErrorString(e));
+        w32[(size_t)l * 4 + i] = p;
+        e = launch_dequant_weight(*ws[i], p, m->stream);
+        if (e != hipSuccess) return undo(LLE_EDEVICE, std::string("f32 weight copy: ") + hipGetErrorString(e));
+      }
+    }
+    hipError_t e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) return undo(LLE_EDEVICE, std::string("f32 weight copy: ") + hipGetErrorString(e));
+    m->w32 = w32;
+  }
+  m->precision = precision;
   return LLE_OK;
 }
 

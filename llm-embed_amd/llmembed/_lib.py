@@ -20,7 +20,7 @@ EXPORTS = [
     "lle_model_set_timing", "lle_model_set_timing_kernel", "lle_model_get_timing", "lle_weight_create", "lle_weight_destroy",
     "lle_weight_dequant", "lle_weight_dequant_f16", "lle_gemm", "lle_gemm_async", "lle_gemm_f16_async",
     "lle_tokenizer_load_gguf", "lle_tokenizer_create", "lle_tokenizer_destroy", "lle_tokenizer_vocab_size",
-    "lle_tokenize", "lle_tokenize_batch", "lle_embed_texts", "lle_embed_packed_async", "lle_embed_packed_noalloc",
+    "lle_tokenize", "lle_tokenize_batch", "lle_embed_texts", "lle_embed_packed_async", "lle_embed_packed_noalloc", "lle_model_set_precision",
 ]
 
 ERRORS = {-1: "EINVAL", -2: "EDEVICE", -3: "ENOMEM", -4: "EUNSUPPORTED", -5: "EIO", -6: "ENOTFOUND"}
@@ -98,6 +98,7 @@ def lib(path: str | None = None):
         "lle_embed_texts": ([P, P, P, P, I32, C.c_char_p, I64, I32, I32, P], I32),
         "lle_embed_packed_async": ([P, P, P, I32, I32, I32, I32, P, P], I32),
         "lle_embed_packed_noalloc": ([P, P, P, I32, I32, I32, I32, P, P], I32),
+        "lle_model_set_precision": ([P, I32], I32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)

@@ -53,6 +53,13 @@ class BertModel:
         check(_lib.lib().lle_forward_hidden(self.h, ptr(ids2), ptr(mask2), B, L, ptr(out)))
         return out[0] if single else out
 
+    def set_precision(self, precision: str):
+        """'f16' (default): MFMA GEMMs on f16 operands, within the reference's tolerance. 'f32':
+        the reference CPU path's own f32 arithmetic in its order (exact f32 weight copies are
+        made on the first switch), embeddings equal to the reference's bit for bit."""
+        code = {"f16": 0, "f32": 1}[precision]
+        check(_lib.lib().lle_model_set_precision(self.h, code))
+
     def set_timing(self, on: bool):
         check(_lib.lib().lle_model_set_timing(self.h, 1 if on else 0))
 
