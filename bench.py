@@ -401,6 +401,28 @@ def main():
                        f"{r['seq_gbs']:.0f} GB/s ({100 * r['seq_hbm_frac']:.1f}% HBM)" if "seq_us" in r else ""))
         del xbuf, ybuf, pbuf, x32buf
 
+        # LLE_PRECISION_F32 (the reference's own f32 arithmetic): config 4 through the host entry
+        # (embeddings compared with the CPU oracle's bit for bit below) and config 1's latency
+        model.set_precision("f32")
+        emb.embed_padded(ids[:2], mask[:2])
+        _hip.synchronize()
+        a = time.perf_counter()
+        out32 = emb.embed_padded(ids, mask)
+        f32_c4_s = time.perf_counter() - a
+        emb.embed(ids1[0], mask1[0])
+        ts = []
+        for _ in range(30):
+            a = time.perf_counter()
+            emb.embed(ids1[0], mask1[0])
+            ts.append(time.perf_counter() - a)
+        model.set_precision("f16")
+        extras["precision_f32"] = dict(c4_emb_per_s=B / f32_c4_s, c4_ms=1e3 * f32_c4_s,
+                                       c1_host_wall_p50_ms=1e3 * float(np.percentile(ts, 50)),
+                                       note="host entries (PCIe included); config-4 rows compared with the CPU "
+                                            "oracle bit for bit in cpu_baseline")
+        log(f"[bench] F32 precision: config 4 {B / f32_c4_s:.0f} emb/s ({1e3 * f32_c4_s:.1f} ms), config 1 "
+            f"{1e3 * float(np.percentile(ts, 50)):.2f} ms (host wall p50)")
+
         # Text path (EmbedBatch over strings): native host tokeniser, then lle_embed_texts'
         # length-ordered batches, against the same texts in input order, 256 per padded batch.
         corpus = synth.texts(4096, seed=0x7E57, min_words=4, max_words=110)
@@ -462,6 +484,11 @@ def main():
                    gpu_vs_cpu_min_cos=float(cos.min()), gpu_vs_cpu_max_abs=max_abs)
         log(f"[bench] cpu oracle {S / cs:.2f} emb/s ({cs:.1f} s); vs GPU over {S} rows: min cos {cos.min():.7f}, "
             f"max abs {max_abs:.2e}")
+        if "precision_f32" in extras:
+            eq = int(np.all(out32[:S].view(np.uint32) == ref.view(np.uint32), axis=1).sum())
+            extras["precision_f32"]["c4_rows_bit_equal_to_cpu"] = f"{eq}/{S}"
+            cpu["f32_precision_rows_bit_equal"] = f"{eq}/{S}"
+            log(f"[bench] F32 precision rows bit-equal to the CPU oracle: {eq}/{S}")
         assert cos.min() >= 0.9999 and max_abs <= 1e-3, "GPU rows outside the parity bar against the oracle"
         # host CPU identity, and config 1 on the CPU: p50 wall time of one L=8 sequence over 50 runs
         model_name, avx512 = None, None

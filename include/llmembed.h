@@ -129,11 +129,11 @@ int32_t lle_embed(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t
 int32_t lle_embed_batch(lle_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t L,
                         int32_t out_dim, float* out);
 
-/* Same on device pointers; returns after enqueueing. The forward runs on the model's own
- * stream (its workspace is shared by every call), ordered by events after the work already
- * queued on `stream` and before the work queued on `stream` later (NULL = the model's stream).
- * Async work must finish before lle_model_destroy. Token ids outside [0, vocab) are clamped and
- * reported by lle_model_status. */
+/* Same on device pointers, enqueued on `stream` (NULL = the model's stream); returns after
+ * enqueueing. A model's forwards share its workspace, so each is ordered after the model's
+ * previous forward: on another stream than that one, `stream` first waits for an event that
+ * marks its end (same stream: no wait). Async work must finish before lle_model_destroy. Token
+ * ids outside [0, vocab) are clamped and reported by lle_model_status. */
 int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int32_t B,
                               int32_t L, int32_t out_dim, float* d_out, void* stream);
 

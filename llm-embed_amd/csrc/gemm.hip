@@ -638,35 +638,20 @@ __device__ __forceinline__ void xcd_tile(int& m0, int& n0) {
   }
 }
 
-// NSX / NSW: LDS stages of the X and of the W tile. Loads run NSX-1 (X) and NSW-1 (W) K steps
-// ahead; NSX = NSW + 1 gives the token tile (the operand with more L2 misses: 50-200 MB of X
-// against a few MB of weights shared by every row tile) one more step of lookahead than the
-// weight tile at the same barrier count, e.g. 3 x 32 KB + 2 x 32 KB = 160 KB for 256 x 256.
-template <int BM, int BN, int WM, int WN, int NSX, int NSW, int EPI, bool MULTI>
+template <int BM, int BN, int WM, int WN, int NS, int EPI, bool MULTI>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FB = TN / 16, TB = TM / 16;
   constexpr int XI = BM / 8 / NW, WI = BN / 8 / NW;  // 1-KB loads per wave per K step
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows per wave");
-  static_assert((NSX == NSW && (NSX == 2 || NSX == 3)) || (NSX == 3 && NSW == 2), "stages");
-  constexpr int PERIOD = NSX == NSW ? NSX : 6;  // K steps per unrolled loop period: lcm(NSX, NSW)
-  // NSX X stages [BM rows x 128 bytes], then NSW W stages [BN rows x 128 bytes], in one LDS
-  // array (stage offsets are compile-time constants); after the K loop the array stages the
-  // epilogue's tile
-  // (NSX == NSW: stage s is [X_s | W_s], so a whole stage is one contiguous block)
-  constexpr int X_STAGE = BM * KSTEP * 2, W_STAGE = BN * KSTEP * 2;
-  constexpr bool SPLIT = NSX != NSW;
-  constexpr int SMEM_BYTES = NSX * X_STAGE + NSW * W_STAGE;
-  static_assert(SMEM_BYTES <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM_BYTES];
+  static_assert(NS == 2 || NS == 3, "stages");
+  // NS stages of [BM X rows | BN W rows] x 128 bytes in one LDS array (stage offsets are
+  // compile-time constants); after the K loop the array stages the epilogue's tile
+  constexpr int X_STAGE = BM * KSTEP * 2, STAGE = X_STAGE + BN * KSTEP * 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
   typedef _Float16 KRow[KSTEP];
-  auto stX = [&](auto S) {
-    return (KRow*)(smem + decltype(S)::value * (SPLIT ? X_STAGE : X_STAGE + W_STAGE));
-  };
-  auto stW = [&](auto S) {
-    return (KRow*)(smem + (SPLIT ? NSX * X_STAGE + decltype(S)::value * W_STAGE
-                                 : decltype(S)::value * (X_STAGE + W_STAGE) + X_STAGE));
-  };
+  auto stX = [&](auto S) { return (KRow*)(smem + decltype(S)::value * STAGE); };
+  auto stW = [&](auto S) { return (KRow*)(smem + decltype(S)::value * STAGE + X_STAGE); };
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -697,7 +682,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   // their accumulators; their cos / sin rows are brought into the stage the last K step leaves
   // free (ROPE_LDS) and read from LDS in the epilogue.
   constexpr bool QKV = EPI == EPI_QKV && !MULTI;
-  constexpr bool ROPE_LDS = QKV && BM == 256 && BN == 256 && NSW == 2;
+  constexpr bool ROPE_LDS = QKV && BM == 256 && BN == 256 && NS == 2;
   constexpr bool PRE = EPI == EPI_QKV && !ROPE_LDS;
   floatx4 eop[PRE ? FB : 1][PRE ? TB : 1];
   int qb[(PRE || QKV) ? TB : 1], qp[(PRE || QKV) ? TB : 1];
@@ -721,20 +706,18 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     const int r = (wave + j * NW) * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
     wo[j] = ((n0 + r) * K + c * 8) * 2;
   }
-  auto issueX = [&](auto S, int kt) {
+  auto issue = [&](auto S, int kt) {
     KRow* sx = stX(S);
+    KRow* sw = stW(S);
 #pragma unroll
     for (int j = 0; j < XI; j++) dma16(rx, &sx[(wave + j * NW) * 8][0], xo[j], kt * KSTEP * 2);
-  };
-  auto issueW = [&](auto S, int kt) {
-    KRow* sw = stW(S);
 #pragma unroll
     for (int j = 0; j < WI; j++) dma16(rw, &sw[(wave + j * NW) * 8][0], wo[j], kt * KSTEP * 2);
   };
   const int lr = lane & 15, lg = lane >> 4;
-  auto compute = [&](auto SX, auto SW, int kt) {
-    const KRow* sw = stW(SW);
-    const KRow* sx = stX(SX);
+  auto compute = [&](auto S, int kt) {
+    const KRow* sw = stW(S);
+    const KRow* sx = stX(S);
     half8 af[2][FB], bf[2][TB];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
@@ -761,46 +744,35 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
       }
     }
   };
-  // Loads of step kt are issued NSW-1 (W) and NSX-1 (X) steps ahead (KT % PERIOD == 0): within
-  // a step the W loads go first, then the X loads. At the top of step kt each wave waits until
-  // only the loads issued after its step-kt operands are in flight (vector loads complete in
-  // issue order) and its LDS reads are done; the barrier then makes every wave's step-kt data
-  // visible and frees the stages read by step kt-1 for the loads issued in step kt. s_barrier is
-  // used bare (with compiler-only fences): __syncthreads() would also wait for every load in
-  // flight.
-  //   NSX == NSW: after step kt's operands come the loads of steps kt+1 .. kt+NS-2.
-  //   NSX == NSW + 1: after W(kt) (issued in step kt-1) comes X(kt+1), issued in the same step.
-  constexpr int VM = NSX == NSW ? (NSX - 2) * (XI + WI) : XI;
+  // NS LDS stages, loads issued NS-1 K steps ahead (KT % NS == 0). At the top of step kt each
+  // wave waits until only the loads of the NS-2 younger steps are in flight (its step-kt loads
+  // have landed) and its LDS reads are done; the barrier then makes every wave's step-kt data
+  // visible and frees the stage of step kt-1 for the loads of step kt+NS-1. s_barrier is used
+  // bare (with compiler-only fences): __syncthreads() would also wait for every load in flight.
+  constexpr int PER_STEP = XI + WI;  // LDS-DMA instructions per wave per K step
+  constexpr int VM = (NS - 2) * PER_STEP;
   static_assert(VM < 64, "vmcnt range");
   constexpr int WAIT = (VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4);  // vmcnt(VM) lgkmcnt(0)
-  auto step = [&](auto I, int kt) {  // I = kt % PERIOD
-    constexpr int i = decltype(I)::value;
-    using SX = std::integral_constant<int, i % NSX>;
-    using SW = std::integral_constant<int, i % NSW>;
-    using SXN = std::integral_constant<int, (i + NSX - 1) % NSX>;  // stage of X(kt + NSX - 1)
-    using SWN = std::integral_constant<int, (i + NSW - 1) % NSW>;  // stage of W(kt + NSW - 1)
-    const bool tail = NSX == NSW ? kt + NSX - 2 < KT : kt + 1 < KT;  // the younger loads exist
-    if (VM > 0 && tail)
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  auto step = [&](auto S, auto SN, int kt) {  // SN: the stage of step kt + NS - 1
+    if (kt + NS - 2 < KT)
       __builtin_amdgcn_s_waitcnt(WAIT);
     else
       __builtin_amdgcn_s_waitcnt(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + NSW - 1 < KT) issueW(SWN{}, kt + NSW - 1);
-    if (kt + NSX - 1 < KT) {
-      issueX(SXN{}, kt + NSX - 1);
-    } else if constexpr (ROPE_LDS && (!SPLIT || SX::value == NSX - 1)) {
-      if (kt == KT - 1 && rsec < 2) {
-        // 64 KB that step kt does not read (last read by steps kt-1 and kt-2): with split
-        // stages the two X stages other than step kt's (X0, X1 when step kt uses X2: KT % 6 == 0),
-        // else the other whole stage. Instruction j of wave w fills tile rows (4 w + j) * 8 +
-        // lane / 8 with the cos / sin row of that token's position (rows past M: row M - 1), the
-        // lane fetching the logical 16-byte chunk (lane % 8) ^ (row & 7)
-        static_assert(2 * 256 * 32 * 4 <= (SPLIT ? 2 * X_STAGE : X_STAGE + W_STAGE), "RoPE rows fit");
-        static_assert(!SPLIT || NSX == 3, "split RoPE staging");
+    if (kt + NS - 1 < KT) {
+      issue(SN, kt + NS - 1);
+    } else if constexpr (ROPE_LDS) {
+      if (kt == KT - 1 && rsec < 2) {  // SN (stage 0) was last read by step kt - 1
+        // instruction j of wave w fills tile rows (4 w + j) * 8 + lane / 8 with the cos / sin
+        // row of that token's position (rows past M: row M - 1), the lane fetching the logical
+        // 16-byte chunk (lane % 8) ^ (row & 7)
         const u32x4_sgpr rc = rsrc_words(p.rope_cos), rs = rsrc_words(p.rope_sin);
-        float* rope = (float*)(smem + (SPLIT ? 0 : (1 - SX::value) * (X_STAGE + W_STAGE)));
+        float* rope = (float*)(smem + decltype(SN)::value * STAGE);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           const int r = (wave * 4 + j) * 8 + (lane >> 3);
@@ -812,29 +784,18 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
         }
       }
     }
-    compute(SX{}, SW{}, kt);
+    compute(S, kt);
   };
-  // prologue: the loads of virtual steps -(max(NSX, NSW) - 1) .. -1, in the same order
-#pragma unroll
-  for (int j = -(NSX > NSW ? NSX : NSW) + 1; j < 0; j++) {
-    const int kw = j + NSW - 1, kx = j + NSX - 1;
-    if (kw >= 0) {
-      if (kw == 0) issueW(std::integral_constant<int, 0>{}, 0);
-      if constexpr (NSW == 3) if (kw == 1) issueW(std::integral_constant<int, 1>{}, 1);
-    }
-    if (kx >= 0) {
-      if (kx == 0) issueX(std::integral_constant<int, 0>{}, 0);
-      if constexpr (NSX == 3) if (kx == 1) issueX(std::integral_constant<int, 1>{}, 1);
-    }
-  }
-  for (int kt = 0; kt < KT; kt += PERIOD) {
-    step(std::integral_constant<int, 0>{}, kt);
-    step(std::integral_constant<int, 1>{}, kt + 1);
-    if constexpr (PERIOD >= 3) step(std::integral_constant<int, 2>{}, kt + 2);
-    if constexpr (PERIOD == 6) {
-      step(std::integral_constant<int, 3>{}, kt + 3);
-      step(std::integral_constant<int, 4>{}, kt + 4);
-      step(std::integral_constant<int, 5>{}, kt + 5);
+  issue(S0{}, 0);
+  if constexpr (NS == 3) issue(S1{}, 1);
+  for (int kt = 0; kt < KT; kt += NS) {
+    if constexpr (NS == 2) {
+      step(S0{}, S1{}, kt);
+      step(S1{}, S0{}, kt + 1);
+    } else {
+      step(S0{}, S2{}, kt);
+      step(S1{}, S0{}, kt + 1);
+      step(S2{}, S1{}, kt + 2);
     }
   }
   if constexpr (ROPE_LDS) {
@@ -1480,34 +1441,25 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
   if (p.M < 1024 && (!multi || p.part)) return launch_small<FMT, 64, EPI>(p, st, reduce);
   if (p.M >= 1024 && p.w16) {
     // 2 stages of 64 KB; f32 outputs from N = 2048 (fewer N tiles leave a round mostly empty)
-    // 256 x 256 tiles: X in 3 stages of 32 KB (loads two K steps ahead), W in 2 (one step
-    // ahead); K steps in periods of 6 (2 + 2 stages when K / 64 is not a multiple of 6)
-    const bool x3 = (p.K / KSTEP) % 6 == 0;
     if (!multi && p.N % 256 == 0 && (p.N >= 4096 || (EPI == EPI_F32 && p.N >= 2048))) {
       dim3 grid(p.N / 256, (p.M + 255) / 256);
-      if (x3)
-        hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 3, 2, EPI, false>), grid, dim3(512), 0, st, p);
-      else
-        hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
+      hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
       return hipGetLastError();
     }
     if constexpr (EPI == EPI_QKV) {
       if (!multi && p.N % 256 == 0 && p.D % 256 == 0 && (p.K / KSTEP) % 2 == 0) {
-        // 256 x 256 tiles, RoPE operands staged in LDS after the K loop
+        // 256 x 256 tiles, 2 stages of 64 KB, RoPE operands staged in LDS after the K loop
         dim3 grid(p.N / 256, (p.M + 255) / 256);
-        if (x3)
-          hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 3, 2, EPI, false>), grid, dim3(512), 0, st, p);
-        else
-          hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
+        hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
         return hipGetLastError();
       }
     }
     if ((p.K / KSTEP) % 3 == 0) {
       dim3 grid(p.N / 128, (p.M + 255) / 256);  // 3 stages of 48 KB
       if (multi)
-        hipLaunchKernelGGL((gemm_h<256, 128, 4, 2, 3, 3, EPI, true>), grid, dim3(512), 0, st, p);
+        hipLaunchKernelGGL((gemm_h<256, 128, 4, 2, 3, EPI, true>), grid, dim3(512), 0, st, p);
       else
-        hipLaunchKernelGGL((gemm_h<256, 128, 4, 2, 3, 3, EPI, false>), grid, dim3(512), 0, st, p);
+        hipLaunchKernelGGL((gemm_h<256, 128, 4, 2, 3, EPI, false>), grid, dim3(512), 0, st, p);
       return hipGetLastError();
     }
   }
@@ -1606,17 +1558,35 @@ hipError_t launch_gemm_lnx(const GemmArgs& a, int epi, const LnPrologue& ln, hip
   }
 }
 
+// Compute units of the current device (blocks of one CU each fill the GPU at this count).
+static int num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0)
+    return 256;
+  return n;
+}
+
 hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
                                 hipStream_t st) {
   const GemmP p = make_params(a);
   const int nch = p.K / kchunk_of(p.K);
   if ((int64_t)p.M * p.K * 2 > INT32_MAX) return hipErrorInvalidValue;  // 32-bit buffer offsets
   // Without the f16 copy the decoding kernel (weights decoded in the loop, 64-row tiles) runs
-  // 128-row tiles on the f16 copy (every format): each block streams the 1.2 MB weight once for
-  // twice the rows of the 64-row kernels (measured 0.102 against 0.114 ms at 32768 tokens);
-  // two 56 KB stages, 256 VGPRs, no spills
-  if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16) {
+  // 128-row tiles on the f16 copy (every format) once they give every CU a block: each block
+  // streams the 1.2 MB weight once for twice the rows of the 64-row kernels (measured 0.103
+  // against 0.112 ms at 32768 tokens); two 56 KB stages, 256 VGPRs, no spills. With fewer rows
+  // the 64-row kernels keep more CUs busy (at 8192 / 16384 tokens: 0.054 / 0.055 ms against
+  // 0.072 / 0.077 for 128-row tiles).
+  if (p.M >= 128 * num_cus() && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16) {
     hipLaunchKernelGGL((gemm_rowln_h<128, 2>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16);
+    return hipGetLastError();
+  }
+  // Q8_0 keeps the decoding kernel: its packed decode is cheap and the block streams half the
+  // weight bytes (measured 0.114 vs 0.124 ms at 32768 tokens); the K-quants' decode is not cheap
+  if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16 && a.w->type != LLE_TYPE_Q8_0 &&
+      (p.K / LN_KS) % 3 == 0) {
+    hipLaunchKernelGGL((gemm_rowln_h<64, 3>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16);
     return hipGetLastError();
   }
   if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) {

@@ -104,22 +104,24 @@ struct lle_model {
   int ws_B = 0;
   lle::Workspace ws;
   int32_t* status = nullptr;  // device status word of async forwards (bits, see lle_model_status)
-  // HIP graphs of small forwards, keyed by shape, rows, pointers and stream. A key is captured
+  // HIP graphs of small forwards, keyed by shape, rows and pointers. A key is captured
   // the second time it runs (a one-off shape, e.g. one text's length, stays eager) and entries
   // are evicted least recently used first.
   struct GraphEntry {
     int B, L, T, out_dim;
     const void *ids, *mask;
     void* out;
-    hipStream_t st;
     hipGraphExec_t exec;  // null: seen once, not captured yet
     uint64_t last_use;
   };
   std::vector<GraphEntry> graphs;
   uint64_t graph_tick = 0;
   bool use_graphs = true;
-  // joins a caller's stream to the model's stream (forwards always run on the latter)
-  hipEvent_t ev_in = nullptr, ev_out = nullptr;
+  // Forwards share the workspace, so each is ordered after the previous one: ev_last marks the
+  // end of the last forward enqueued, on last_stream; a forward on another stream waits for it.
+  hipEvent_t ev_last = nullptr;
+  hipStream_t last_stream = nullptr;
+  bool ev_last_valid = false;
   // timing
   bool timing = false;
   std::string timing_only;  // non-empty: only this kernel class is bracketed, read at get_timing
@@ -166,6 +168,8 @@ static void ws_free(lle_model* m) {
     ptr = (decltype(ptr))p_;                                                            \
   } while (0)
 
+static int wait_forwards(lle_model* m);
+
 // Grow-only workspace for a [B][L] batch whose forward runs on `rows` token rows (B*L, or fewer
 // when padding is packed away).
 static int ensure_ws(lle_model* m, int B, int L, int64_t rows = -1) {
@@ -180,7 +184,7 @@ static int ensure_ws(lle_model* m, int B, int L, int64_t rows = -1) {
   if (T <= m->ws_T && heads <= m->ws_heads && part <= m->ws_part && B <= m->ws_B) return LLE_OK;
   const size_t nT = std::max(T, m->ws_T), nH = std::max(heads, m->ws_heads), nP = std::max(part, m->ws_part);
   const int nB = std::max(B, m->ws_B);
-  LLE_HIP(hipStreamSynchronize(m->stream));
+  if (int rc = wait_forwards(m)) return rc;
   ws_free(m);
   Workspace& w = m->ws;
   WS_ALLOC(w.h, nT * m->D * 4);
@@ -291,6 +295,33 @@ struct Packing {
   const int32_t* seq_off;
 };
 
+// Forwards of one model share its workspace, so each must run after the previous one on the
+// device, whichever streams the callers use. Every forward ends by recording ev_last on its
+// stream; a forward on a different stream first waits for that event (on one stream the order
+// is already given, so a single-stream caller pays nothing). A stream that a caller is
+// capturing into a graph is left alone: its graph defines its own order.
+static bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+static int order_begin(lle_model* m, hipStream_t st) {
+  if (m->ev_last_valid && st != m->last_stream && !capturing(st)) LLE_HIP(hipStreamWaitEvent(st, m->ev_last, 0));
+  return LLE_OK;
+}
+static int order_end(lle_model* m, hipStream_t st) {
+  if (capturing(st)) return LLE_OK;
+  LLE_HIP(hipEventRecord(m->ev_last, st));
+  m->last_stream = st;
+  m->ev_last_valid = true;
+  return LLE_OK;
+}
+// Waits for every forward enqueued so far (before the workspace is freed or replaced).
+static int wait_forwards(lle_model* m) {
+  if (m->ev_last_valid) LLE_HIP(hipEventSynchronize(m->ev_last));
+  LLE_HIP(hipStreamSynchronize(m->stream));
+  return LLE_OK;
+}
+
 static void ex_free(lle_model* m) {
   float* bufs[] = {m->ex_h, m->ex_q, m->ex_k, m->ex_v, m->ex_att, m->ex_g};
   for (float* b : bufs)
@@ -302,7 +333,7 @@ static void ex_free(lle_model* m) {
 // f32 activations of the exact forward for `rows` token rows (grow-only).
 static int ensure_exact_ws(lle_model* m, size_t rows) {
   if (rows <= m->ex_T) return LLE_OK;
-  LLE_HIP(hipStreamSynchronize(m->stream));
+  if (int rc = wait_forwards(m)) return rc;
   ex_free(m);
   const size_t D = m->D, F = m->F;
   float** dst[] = {&m->ex_h, &m->ex_q, &m->ex_k, &m->ex_v, &m->ex_att, &m->ex_g};
@@ -544,16 +575,15 @@ constexpr size_t GRAPH_KEYS = 128;  // keys remembered (captured or seen once)
 static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int B, int L, int out_dim,
                        float* d_out, hipStream_t st, const Packing* pk = nullptr) {
   const int T = pk ? pk->T : B * L;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   // a stream the caller is capturing already records this forward into the caller's graph
   if (m->timing || !m->use_graphs || !st || (int64_t)B * L > GRAPH_MAX_TOKENS || m->precision != LLE_PRECISION_F16 ||
-      hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+      capturing(st))
     return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   const uint64_t now = ++m->graph_tick;
   lle_model::GraphEntry* e = nullptr;
   for (auto& g : m->graphs)
     if (g.B == B && g.L == L && g.T == T && g.out_dim == out_dim && g.ids == d_ids && g.mask == d_mask &&
-        g.out == d_out && g.st == st) {
+        g.out == d_out) {
       e = &g;
       break;
     }
@@ -565,14 +595,19 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
   if (!e) {  // first sighting: run eagerly, remember the key
     if (m->graphs.size() >= GRAPH_KEYS) {
       auto lru = std::min_element(m->graphs.begin(), m->graphs.end(),
-                                  [](const lle_model::GraphEntry& a, const lle_model::GraphEntry& b) { return a.last_use < b.last_use; });
+                                  [](const lle_model::GraphEntry& a, const lle_model::GraphEntry& b) {
+                                    return a.last_use < b.last_use;
+                                  });
       if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
       m->graphs.erase(lru);
     }
-    m->graphs.push_back({B, L, T, out_dim, d_ids, d_mask, d_out, st, nullptr, now});
+    m->graphs.push_back({B, L, T, out_dim, d_ids, d_mask, d_out, nullptr, now});
     return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
   }
-  // second sighting: capture, keeping at most GRAPH_EXECS instantiated graphs
+  // second sighting: capture, keeping at most GRAPH_EXECS instantiated graphs. The capture runs
+  // on the model's own non-blocking stream (held under the model's mutex, so nothing else is
+  // enqueued on it meanwhile, and no other thread's legacy default stream waits on it); the
+  // graph is then launched on the caller's stream.
   e->last_use = now;
   const size_t idx = (size_t)(e - m->graphs.data());
   size_t n_exec = 0;
@@ -585,31 +620,24 @@ static int run_forward(lle_model* m, const int32_t* d_ids, const int32_t* d_mask
     lru->exec = nullptr;
   }
   hipGraph_t graph = nullptr;
-  if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
-    (void)hipGetLastError();
-    m->use_graphs = false;  // capture unsupported here: eager from now on
-    return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
-  }
-  const int rc = forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
-  const hipError_t ce = hipStreamEndCapture(st, &graph);
-  if (rc != LLE_OK) {  // a failing forward is reported; it does not turn graphs off
-    if (graph) (void)hipGraphDestroy(graph);
-    (void)hipGetLastError();
-    return rc;
-  }
   hipGraphExec_t exec = nullptr;
-  if (ce == hipSuccess && graph && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess) {
-    (void)hipGraphDestroy(graph);
-    m->graphs[idx].exec = exec;
-    LLE_HIP(hipGraphLaunch(exec, st));
-    return LLE_OK;
+  if (hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+    const int rc = forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, m->stream, pk);
+    const hipError_t ce = hipStreamEndCapture(m->stream, &graph);
+    if (rc == LLE_OK && ce == hipSuccess && graph && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess) {
+      (void)hipGraphDestroy(graph);
+      m->graphs[idx].exec = exec;
+      LLE_HIP(hipGraphLaunch(exec, st));
+      return LLE_OK;
+    }
   }
+  // the capture did not succeed: this forward runs eagerly (a genuine error shows there)
   if (graph) (void)hipGraphDestroy(graph);
   (void)hipGetLastError();
-  m->use_graphs = false;
   return forward(m, m->ws, d_ids, d_mask, B, L, out_dim, d_out, st, pk);
 }
 
+// Bytes of one head buffer (Q, K or V^T) of a [B][L] batch: [B][H][Lp][64] f16.
 static int64_t heads_bytes(const lle_model* m, int64_t B, int64_t L) { return B * m->H * ((L + 63) / 64 * 64) * 64 * 2; }
 // The attention grid's z dimension is the sequence index.
 constexpr int kMaxBatch = 65535;
@@ -681,6 +709,7 @@ static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L, packed ? (int64_t)pids.size() : -1))) return rc;
   hipStream_t st = m->stream;
+  if ((rc = order_begin(m, st))) return rc;
   Packing pk{(int)pids.size(), m->ws.tokrow, m->ws.seq_off};
   if (packed) {
     LLE_HIP(hipMemcpyAsync(m->ws.ids, pids.data(), pids.size() * 4, hipMemcpyHostToDevice, st));
@@ -698,6 +727,7 @@ static int run_host(lle_model* m, const int32_t* ids, const int32_t* mask, int B
   if (hidden)
     LLE_HIP(hipMemcpyAsync(hidden, m->precision == LLE_PRECISION_F32 ? m->ex_h : m->ws.h, T * m->D * 4,
                            hipMemcpyDeviceToHost, st));
+  if ((rc = order_end(m, st))) return rc;
   // host buffers above (pids, prow, soff, ones) must outlive the copies
   LLE_HIP(hipStreamSynchronize(st));
   if (m->timing && m->timing_only.empty()) collect_timing(m);
@@ -787,7 +817,7 @@ static int upload_vec(lle_model* m, const lle_tensor& t, int n, float** out) {
 static void destroy_model(lle_model* m) {
   if (!m) return;
   (void)hipSetDevice(m->device);
-  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  if (m->stream) (void)wait_forwards(m);
   ws_free(m);  // also destroys cached graphs
   ex_free(m);
   for (float* p : m->w32)
@@ -799,8 +829,7 @@ static void destroy_model(lle_model* m) {
   }
   for (auto e : m->event_pool) (void)hipEventDestroy(e);
   if (m->status) (void)hipFree(m->status);
-  if (m->ev_in) (void)hipEventDestroy(m->ev_in);
-  if (m->ev_out) (void)hipEventDestroy(m->ev_out);
+  if (m->ev_last) (void)hipEventDestroy(m->ev_last);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
 }
@@ -864,9 +893,10 @@ static int create_model(const lle_model_desc* d, lle_model** out) {
     return code;
   };
   if (hipSetDevice(m->device) != hipSuccess) return bail(fail(LLE_EDEVICE, "hipSetDevice failed"));
-  if (hipStreamCreate(&m->stream) != hipSuccess) return bail(fail(LLE_EDEVICE, "hipStreamCreate failed"));
-  if (hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming) != hipSuccess)
+  // non-blocking: no other thread's legacy default stream waits on it (graphs are captured here)
+  if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess)
+    return bail(fail(LLE_EDEVICE, "hipStreamCreate failed"));
+  if (hipEventCreateWithFlags(&m->ev_last, hipEventDisableTiming) != hipSuccess)
     return bail(fail(LLE_EDEVICE, "hipEventCreate failed"));
   if (hipMalloc((void**)&m->status, 4) != hipSuccess) return bail(fail(LLE_ENOMEM, "hipMalloc status"));
   (void)hipMemset(m->status, 0, 4);
@@ -1180,23 +1210,6 @@ int32_t lle_forward_hidden(lle_model* m, const int32_t* ids, const int32_t* mask
   return run_host(m, ids, mask, B, L, m ? m->D : 0, nullptr, hidden);
 }
 
-// Async forwards run on the model's stream whatever stream the caller passes: the workspace is
-// the model's, so two calls must not overlap on the device. The caller's stream is joined by
-// events: the model's stream first waits for the caller's earlier work, and the caller's stream
-// then waits for the forward.
-static int join_in(lle_model* m, hipStream_t cs) {
-  if (cs == m->stream) return LLE_OK;
-  LLE_HIP(hipEventRecord(m->ev_in, cs));
-  LLE_HIP(hipStreamWaitEvent(m->stream, m->ev_in, 0));
-  return LLE_OK;
-}
-static int join_out(lle_model* m, hipStream_t cs) {
-  if (cs == m->stream) return LLE_OK;
-  LLE_HIP(hipEventRecord(m->ev_out, m->stream));
-  LLE_HIP(hipStreamWaitEvent(cs, m->ev_out, 0));
-  return LLE_OK;
-}
-
 int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t* d_mask, int32_t B, int32_t L,
                               int32_t out_dim, float* d_out, void* stream) {
   int rc = check_batch(m, B, L);
@@ -1208,10 +1221,10 @@ int32_t lle_embed_batch_async(lle_model* m, const int32_t* d_ids, const int32_t*
     return fail(LLE_EUNSUPPORTED, "F32 precision needs each sequence's length: use lle_embed_packed_async or a host entry");
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L))) return rc;
-  const hipStream_t cs = stream ? (hipStream_t)stream : m->stream, st = m->stream;
-  if ((rc = join_in(m, cs))) return rc;
+  const hipStream_t st = stream ? (hipStream_t)stream : m->stream;
+  if ((rc = order_begin(m, st))) return rc;
   if ((rc = run_forward(m, d_ids, d_mask, B, L, out_dim, d_out, st))) return rc;
-  if ((rc = join_out(m, cs))) return rc;
+  if ((rc = order_end(m, st))) return rc;
   if (m->timing && m->timing_only.empty()) {
     LLE_HIP(hipStreamSynchronize(st));
     collect_timing(m);
@@ -1229,12 +1242,12 @@ int32_t lle_embed_packed_async(lle_model* m, const int32_t* d_ids, const int32_t
   std::lock_guard<std::mutex> lk(m->mu);
   LLE_HIP(hipSetDevice(m->device));
   if ((rc = ensure_ws(m, B, L, T))) return rc;
-  const hipStream_t cs = stream ? (hipStream_t)stream : m->stream, st = m->stream;
-  if ((rc = join_in(m, cs))) return rc;
+  const hipStream_t st = stream ? (hipStream_t)stream : m->stream;
+  if ((rc = order_begin(m, st))) return rc;
   LAUNCH(launch_pack_tables(d_seq_off, B, T, L, m->ws.seq_off, m->ws.tokrow, m->ws.mask, m->status, st));
   Packing pk{T, m->ws.tokrow, m->ws.seq_off};
   if ((rc = run_forward(m, d_ids, m->ws.mask, B, L, out_dim, d_out, st, &pk))) return rc;
-  if ((rc = join_out(m, cs))) return rc;
+  if ((rc = order_end(m, st))) return rc;
   if (m->timing && m->timing_only.empty()) {
     LLE_HIP(hipStreamSynchronize(st));
     collect_timing(m);
@@ -1257,7 +1270,7 @@ int32_t lle_model_set_precision(lle_model* m, int32_t precision) {
     return fail(LLE_EINVAL, "precision must be LLE_PRECISION_F16 or LLE_PRECISION_F32");
   std::lock_guard<std::mutex> lk(m->mu);
   LLE_HIP(hipSetDevice(m->device));
-  LLE_HIP(hipStreamSynchronize(m->stream));
+  if (int rc = wait_forwards(m)) return rc;
   if (precision == LLE_PRECISION_F32 && m->w32.empty()) {
     // PreDequant (internal/embed/bert.go:542-576): every projection dequantised once to f32
     // [N][K] by the GEMM's own decoder (bit-exact with DequantWeightMatrix)

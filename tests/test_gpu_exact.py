@@ -114,6 +114,14 @@ def test_exact_full_model_config3_rows(gpu, full_spec):
     check_exact(e.embed_padded(ids, mask), o.embed_batch(ids, mask), "exact c3 x16")
 
 
+def test_exact_full_model_config4_all_rows(gpu, full_spec):
+    """Config 4 at full size (B=256, L=128, 12 layers, Q8_0): all 256 rows bit-equal to the
+    oracle's."""
+    e, o = models(full_spec, "Q8_0", synth.CONFIG_SEED + 4)
+    ids, mask = synth.config_inputs(4)
+    check_exact(e.embed_padded(ids, mask), o.embed_batch(ids, mask), "exact c4 all rows")
+
+
 def test_exact_mode_rejections_and_switch_back(gpu, small_spec):
     """F32 mode refuses the entries that cannot know each sequence's length; switching back to
     F16 gives the F16 rows again."""
