@@ -186,8 +186,16 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
   }
   const float scale = 0.125f;  // float32(1/sqrt(64)), bert.go:362
 
-  float m_run = -INFINITY, lsum = 0.f, smin = INFINITY;
+  float m_run = -INFINITY, smin = INFINITY;
   floatx4 o[4];
+  // row sums of P on the matrix core: an all-ones V^T fragment against the same P^T fragment
+  // gives, in every row of its 16 x 16 result, the sum over the tile's keys of each query's f16
+  // probabilities (the weights the P.V MFMAs use), so the normalisation divides by exactly the
+  // weights the numerator summed
+  floatx4 osum;
+  half8 ones;
+#pragma unroll
+  for (int i = 0; i < 8; i++) ones[i] = (_Float16)1.0f;
 
   auto sstore = [&](int buf) {
 #pragma unroll
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
     }
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    lsum = 0.f;
+    osum = floatx4{0.f, 0.f, 0.f, 0.f};
     smin = INFINITY;
     const float m_fix = m_run;
 
@@ -269,18 +277,19 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
       } else {
         mref = m_fix;
       }
-      float e[16];
-      float ps = 0.f;
+      float e[16], kept[16];
 #pragma unroll
       for (int i = 0; i < 16; i++) {  // branch-free: exp of a dropped key (z < -10) is discarded
         const float z = fmaf(s[i], scale, -mref);
         const bool keep = z >= -10.f;
         const float ex = __expf(z);
         e[i] = keep ? ex : 0.f;
-        smin = fminf(smin, keep ? s[i] : INFINITY);  // smallest kept score (exact, order-free)
-        ps += e[i];
+        kept[i] = keep ? s[i] : INFINITY;
       }
-      lsum = lsum * alpha + ps;
+      // smallest kept score (exact, order-free), two scores per step (v_min3)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) smin = fminf(smin, fminf(kept[i], kept[i + 1]));
+      osum *= alpha;
 #pragma unroll
       for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
       // P^T fragments: keys 32j + 8g + 0..7
@@ -305,6 +314,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
             o[dt] = mfma16(vf, pf, o[dt]);
           }
         }
+        osum = mfma16(ones, pf, osum);
       }
       if (more) sstore(buf ^ 1);  // buffer buf^1 was last read in iteration kt-1
       __syncthreads();
@@ -317,8 +327,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
     }
   }
 
-  float tot = lsum + __shfl_xor(lsum, 16);
-  tot += __shfl_xor(tot, 32);
+  const float tot = osum[0];  // every row of osum holds the query's sum over all keys
   if (q < Lk) {
     const float inv = 1.f / tot;
     __half* dst = a.out + (orow + q) * a.D + h * HD + 4 * g;
