@@ -8,10 +8,13 @@
 // Keys stream through LDS 64 at a time; S = K Q^T and O^T = V^T P^T run on
 // v_mfma_f32_16x16x32_f16.
 //
-// Cutoff with an online max: a key is kept when s - m_run >= -10, with m_run the running max.
-// Every key the reference keeps is kept (m_run <= m_final). A kept key the reference would drop
-// has s - m_final < -10; the smallest kept score per query detects that case after the pass,
-// and the block then repeats the pass with m_final fixed, which is exactly the reference rule.
+// Cutoff with an online max: a key is kept when s - m_run >= -10, with m_run the running max
+// (tested exactly as a threshold on the unscaled score, keep_threshold). The exponentials use a
+// reference point that trails m_run by a bounded amount, so the accumulators are rescaled only
+// when the maximum moves far. Every key the reference keeps is kept (m_run <= m_final). A kept
+// key the reference would drop has s - m_final < -10; the smallest kept score per query detects
+// that case after the pass, and the block then repeats the pass with m_final fixed, which is
+// exactly the reference rule.
 // Key tiles outside [first valid key, last valid key] hold only masked keys; they contribute
 // exact zeros and are skipped (all tiles are visited when a sequence has no valid key, where
 // the reference's softmax is uniform).
@@ -47,6 +50,26 @@ __device__ __forceinline__ const __half* uniform_ptr(const __half* p) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return (const __half*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
+// Smallest f32 not below y (y is computed in f64; see keep_threshold).
+__device__ __forceinline__ float ceil_f32(double y) {
+  float f = (float)y;
+  if ((double)f < y) {
+    unsigned int u = __float_as_uint(f);
+    u = f == 0.f ? 1u : (f > 0.f ? u + 1u : u - 1u);  // one step towards +inf
+    f = __uint_as_float(u);
+  }
+  return f;
+}
+// Keep rule of the reference's softmax, fl(s - m) >= -10 with s = u / 8 (exact), as a threshold
+// on the unscaled score u. fl(x) >= -10 exactly when x >= -10 - 2^-21 (the f32 spacing below 10
+// is 2^-20 and a tie rounds to the even -10), so a key is kept exactly when
+// u >= 8 * ceil_f32(m - 10 - 2^-21). m is f32, and m + (-10 - 2^-21) is exact in f64 for
+// 2^-26 <= |m| < 2^31; for smaller |m| no f32 lies within the f64 rounding error of the sum.
+__device__ __forceinline__ float keep_threshold(float m_u) {
+  const double y = (double)(m_u * 0.125f) + (-10.0 - 0x1p-21);
+  return 8.f * ceil_f32(y);
+}
+
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) {
   const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
   return uint4{t.x, t.y, t.z, t.w};
@@ -58,6 +81,11 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) 
 template <int NW, bool EARLY>
 __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(AttnArgs a) {
   constexpr int NT = NW * 64, AQB = NW * 16;
+  // Long rows (8-wave blocks) test the keep rule as a per-query threshold on the unscaled score,
+  // recomputed once per key tile (one f64 chain) in place of a fused multiply-add per score.
+  // Short rows (one key tile) compare directly, off that chain's latency. Both keep exactly the
+  // same keys, so every output bit is the same either way.
+  constexpr bool THR = NW == 8;
   constexpr int CPT = (AK * HD / 8) / NT;  // 16-byte chunks of each tile per thread
   __shared__ __attribute__((aligned(16))) _Float16 sK[2][AK][HD + APAD];   // [key][dim]
   __shared__ __attribute__((aligned(16))) _Float16 sV[2][HD][AK + APAD];   // [dim][key]
@@ -134,6 +162,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
   // scan's remaining mask loads (loads complete in issue order).
   __shared__ int sLo[NW], sHi[NW];
   int klo, khi;
+  bool novalid;
   {
     const int32_t* mrow = a.mask + (size_t)b * L;
     int lo = L, hi = -1, i0 = tid;
@@ -172,6 +201,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
     }
     klo = hi < 0 ? 0 : lo;
     khi = hi < 0 ? L : hi + 1;
+    novalid = hi < 0;
   }
   const int t0 = klo / AK, t1 = (khi + AK - 1) / AK;
   if (qt * AQB >= khi) {
@@ -185,8 +215,20 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
     return;
   }
   const float scale = 0.125f;  // float32(1/sqrt(64)), bert.go:362
+  // exp(s - m) = 2^((u - 8 m) * log2(e) / 8): one fmaf with c1 = fl(log2 e) / 8 (exact scaling)
+  const float c1 = 1.44269504f * 0.125f;
+  // A masked key's unscaled score: -8e9 (s = -1e9 exactly). A sequence without a valid key has
+  // every key masked, its softmax is uniform (and its rows are never pooled); 0 then gives the
+  // same uniform weights without the cancellation of -8e9 * c1 against the reference point.
+  const float mval = novalid ? 0.f : -8e9f;
+  // Rows of P are scaled by 2^(-m_ref * c1), m_ref a query's running maximum (unscaled) as of its
+  // last rescale. The accumulators are rescaled only when the running maximum has moved more
+  // than kTau past m_ref, so P stays below e^(kTau / 8) (f16 range) and most key tiles skip the
+  // rescale. Each query decides alone (its lanes hold the same maxima), so its arithmetic does
+  // not depend on the other queries of its wave.
+  constexpr float kTau = 64.f;
 
-  float m_run = -INFINITY, smin = INFINITY;
+  float m_u = -INFINITY, smin = INFINITY;  // running maximum and smallest kept score (unscaled)
   floatx4 o[4];
   // row sums of P on the matrix core: an all-ones V^T fragment against the same P^T fragment
   // gives, in every row of its 16 x 16 result, the sum over the tile's keys of each query's f16
@@ -222,7 +264,10 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
     for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     osum = floatx4{0.f, 0.f, 0.f, 0.f};
     smin = INFINITY;
-    const float m_fix = m_run;
+    // the fixed pass uses the final maximum for the keep rule and as the reference point
+    float m_ref = fixed ? m_u : -INFINITY;
+    float nb = -(m_ref * c1);
+    float thr = fixed && THR ? keep_threshold(m_u) : 0.f;
 
     __syncthreads();  // the buffers of a previous pass are no longer read
     if (!EARLY || fixed || t0 != 0) gload(t0);  // else tile 0 is already in registers
@@ -260,38 +305,56 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
         for (int t = 0; t < 4; t++)
 #pragma unroll
           for (int r = 0; r < 4; r++)
-            if (sMask[buf][32 * (t >> 1) + 8 * g + 4 * (t & 1) + r] == 0) s[4 * t + r] = -8e9f;
+            if (sMask[buf][32 * (t >> 1) + 8 * g + 4 * (t & 1) + r] == 0) s[4 * t + r] = mval;
       }
-      float tmax = -INFINITY;
+      // the tile's smallest score: when it is kept, so is every key of the tile
+      float tmin = INFINITY;
 #pragma unroll
-      for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, s[i]);
-      tmax *= scale;
-      float alpha = 1.f, mref;
+      for (int i = 0; i < 16; i += 2) tmin = fminf(tmin, fminf(s[i], s[i + 1]));
       if (!fixed) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, s[i]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
-        alpha = (m_new == m_run) ? 1.f : __expf(m_run - m_new);
-        m_run = m_new;
-        mref = m_new;
+        m_u = fmaxf(m_u, tmax);
+        if constexpr (THR) thr = keep_threshold(m_u);
+        const bool need = m_u > m_ref + kTau;  // always on the first tile (m_ref = -inf)
+        if (__any(need)) {
+          const float alpha = need ? __builtin_amdgcn_exp2f((m_ref - m_u) * c1) : 1.f;
+          osum *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+          m_ref = need ? m_u : m_ref;
+          nb = -(m_ref * c1);
+        }
+      }
+      // The keep rule fl(s - m) >= -10, tested as u >= thr (THR) or directly: the same keys.
+      const float m_s = m_u * scale;
+      auto keeps = [&](float u) {
+        if constexpr (THR)
+          return u >= thr;
+        else
+          return fmaf(u, scale, -m_s) >= -10.f;
+      };
+      float e[16];
+      if (__any(!keeps(tmin))) {
+        // some query of the wave drops a key of this tile: exp of a dropped key is discarded,
+        // and the smallest kept score is taken over the kept keys (for a query that dropped
+        // nothing both are what the branch below computes)
+        tmin = INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const bool keep = keeps(s[i]);
+          const float ex = __builtin_amdgcn_exp2f(fmaf(s[i], c1, nb));
+          e[i] = keep ? ex : 0.f;
+          tmin = fminf(tmin, keep ? s[i] : INFINITY);
+        }
       } else {
-        mref = m_fix;
+#pragma unroll
+        for (int i = 0; i < 16; i++) e[i] = __builtin_amdgcn_exp2f(fmaf(s[i], c1, nb));
       }
-      float e[16], kept[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) {  // branch-free: exp of a dropped key (z < -10) is discarded
-        const float z = fmaf(s[i], scale, -mref);
-        const bool keep = z >= -10.f;
-        const float ex = __expf(z);
-        e[i] = keep ? ex : 0.f;
-        kept[i] = keep ? s[i] : INFINITY;
-      }
-      // smallest kept score (exact, order-free), two scores per step (v_min3)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) smin = fminf(smin, fminf(kept[i], kept[i + 1]));
-      osum *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+      smin = fminf(smin, tmin);  // smallest kept score (exact, order-free)
       // P^T fragments: keys 32j + 8g + 0..7
 #pragma unroll
       for (int j = 0; j < 2; j++) {
@@ -322,7 +385,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
     if (!fixed) {
       float sm = fminf(smin, __shfl_xor(smin, 16));
       sm = fminf(sm, __shfl_xor(sm, 32)) * scale;
-      const bool flag = qvalid && (sm - m_run < -10.f);
+      const bool flag = qvalid && (sm - m_u * scale < -10.f);
       if (__any(flag)) sRedo = 1;  // benign race: every writer stores 1
     }
   }
