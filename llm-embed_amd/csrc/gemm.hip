@@ -1578,18 +1578,26 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
   // against 0.112 ms at 32768 tokens); two 56 KB stages, 256 VGPRs, no spills. With fewer rows
   // the 64-row kernels keep more CUs busy (at 8192 / 16384 tokens: 0.054 / 0.055 ms against
   // 0.072 / 0.077 for 128-row tiles).
+  // The full-row kernels stream the whole weight through every block, so a block takes about as
+  // long as two 256 x 128 tiles of the split path (tile GEMM with the residual epilogue, then the
+  // LayerNorm kernel). Below the row count at which the split path's tiles fill one round of the
+  // CUs, the full-row kernels leave CUs idle and the split path is faster (bit-identical rows;
+  // config 3's 8192 rows: 0.038 against 0.055 ms); from there on the full-row kernels win
+  // (16384 rows: 0.055 against 0.064 ms).
+  const bool split_mid = p.w16 && p.M >= 1024 && (p.K / KSTEP) % 3 == 0 && p.N % 128 == 0 &&
+                         (int64_t)((p.M + 255) / 256) * (p.N / 128) <= num_cus();
   if (p.M >= 128 * num_cus() && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16) {
     hipLaunchKernelGGL((gemm_rowln_h<128, 2>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16);
     return hipGetLastError();
   }
   // Q8_0 keeps the decoding kernel: its packed decode is cheap and the block streams half the
   // weight bytes (measured 0.114 vs 0.124 ms at 32768 tokens); the K-quants' decode is not cheap
-  if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16 && a.w->type != LLE_TYPE_Q8_0 &&
+  if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16 && a.w->type != LLE_TYPE_Q8_0 &&
       (p.K / LN_KS) % 3 == 0) {
     hipLaunchKernelGGL((gemm_rowln_h<64, 3>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16);
     return hipGetLastError();
   }
-  if (p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) {
+  if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) {
     const dim3 grid((p.M + 63) / 64), blk(512);
     switch (a.w->type) {
       case LLE_TYPE_Q8_0: hipLaunchKernelGGL((gemm_rowln<8, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
