@@ -70,6 +70,24 @@ __device__ __forceinline__ float keep_threshold(float m_u) {
   return 8.f * ceil_f32(y);
 }
 
+// Maximum / minimum over lanes l, l ^ 16, l ^ 32 and l ^ 48 of a wave (the four lanes that hold
+// one query's scores). v_permlane16_swap / v_permlane32_swap exchange 16-lane rows between two
+// registers without an LDS round trip; afterwards each lane holds its own value in one register
+// and its partner's in the other. max and min are order-free, so the result is the xor
+// butterfly's bit for bit.
+__device__ __forceinline__ float max_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float min_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fminf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fminf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) {
   const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
   return uint4{t.x, t.y, t.z, t.w};
@@ -315,9 +333,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, s[i]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        m_u = fmaxf(m_u, tmax);
+        m_u = fmaxf(m_u, max_rows(tmax));
         if constexpr (THR) thr = keep_threshold(m_u);
         const bool need = m_u > m_ref + kTau;  // always on the first tile (m_ref = -inf)
         if (__any(need)) {
@@ -383,8 +399,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(Att
       __syncthreads();
     }
     if (!fixed) {
-      float sm = fminf(smin, __shfl_xor(smin, 16));
-      sm = fminf(sm, __shfl_xor(sm, 32)) * scale;
+      const float sm = min_rows(smin) * scale;
       const bool flag = qvalid && (sm - m_u * scale < -10.f);
       if (__any(flag)) sRedo = 1;  // benign race: every writer stores 1
     }
