@@ -19,147 +19,9 @@
 #include <climits>
 #include <type_traits>
 
-#include "deq_device.h"
-#include "lle_internal.h"
-#include "row_device.h"
+#include "gemm_small.h"
 
 namespace lle {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-constexpr int KSTEP = 64;   // K per LDS stage
-
-struct GemmP {
-  WPlanes w;
-  const __half* x;
-  int M, N, K;
-  float* y;
-  __half* q;
-  __half* k;
-  __half* vt;
-  const float* rope_cos;
-  const float* rope_sin;
-  int L, Lp, H, D;
-  __half* g;
-  float* part;  // split-K partials [K/kchunk][M][N]
-  const __half* w16;  // resident f16 copy of the weights [N][K], or null
-  LnPrologue ln;      // LayerNorm prologue of the small-M kernel
-  const int32_t* tokrow;  // packed rows: row m is padded token tokrow[m] (null: m)
-};
-
-// GeLU with the reference's rational tanh (internal/ggml/ops_simd.go:27-42):
-//   t = 0.7978845608 v (1 + 0.044715 v v),  tanh ~ t (27 + t^2) / (27 + 9 t^2),  +-1 past |t| 4.97,
-//   0.5 v (1 + tanh).
-// Written for the up/gate GEMM's epilogue, which runs it on 100 M values per launch with the
-// matrix cores idle: the quotient uses the hardware reciprocal (v_rcp_f32, 1 ulp) instead of a
-// correctly rounded division, three of the multiply-adds are fused, and the clamp is a select
-// (a branch per value before). Each changes the result by an ulp or so of f32 before it is
-// rounded to f16 (2^-11); every GEMM path calls this one function, so they stay bit-identical.
-__device__ __forceinline__ float gelu_r(float v) {
-  const float t = (0.7978845608f * v) * fmaf(0.044715f * v, v, 1.0f);
-  const float t2 = t * t;
-  float r = t * (27.0f + t2) * __builtin_amdgcn_rcpf(fmaf(9.0f, t2, 27.0f));
-  asm("" : "+v"(r));  // computed for every value: otherwise the select becomes a branch around it
-  const float th = fabsf(t) > 4.97f ? copysignf(1.0f, t) : r;
-  const float hv = 0.5f * v;
-  return fmaf(hv, th, hv);
-}
-
-// Operands an epilogue reads from memory for features f..f+3 of token m: the residual
-// (EPI_RESID) or the RoPE cos/sin pairs (EPI_QKV, Q and K sections). The small-M kernel issues
-// these loads before its main loop so that they do not add a round trip at the end.
-template <int EPI>
-__device__ __forceinline__ floatx4 epi_operands(const GemmP& p, int m, int f) {
-  if constexpr (EPI == EPI_RESID) {
-    return *(const floatx4*)(p.y + (size_t)m * p.N + f);
-  } else if constexpr (EPI == EPI_QKV) {
-    const int sec = f / p.D, e = (f - sec * p.D) & 63;
-    const int r = p.tokrow ? p.tokrow[m] : m;
-    const int pos = r - (r / p.L) * p.L;
-    if (sec < 2) {
-      const float* cr = p.rope_cos + (size_t)pos * 32 + (e >> 1);
-      const float* sr = p.rope_sin + (size_t)pos * 32 + (e >> 1);
-      return floatx4{cr[0], sr[0], cr[1], sr[1]};
-    }
-    return floatx4{0.f, 0.f, 0.f, 0.f};
-  } else {
-    return floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-}
-
-// Epilogue for 4 consecutive output features f..f+3 (f % 4 == 0) of token m; `o` holds what
-// epi_operands returned for the same (m, f).
-template <int EPI>
-__device__ __forceinline__ void epilogue_with(const GemmP& p, int m, int f, floatx4 v, floatx4 o) {
-  if constexpr (EPI == EPI_F32) {
-    *(floatx4*)(p.y + (size_t)m * p.N + f) = v;
-  } else if constexpr (EPI == EPI_RESID) {
-    // hiddens[i][j] += out[i][j]  (internal/embed/bert.go:262-264, 276-278)
-    floatx4 h = o;
-    h.x = h.x + v.x; h.y = h.y + v.y; h.z = h.z + v.z; h.w = h.w + v.w;
-    *(floatx4*)(p.y + (size_t)m * p.N + f) = h;
-  } else if constexpr (EPI == EPI_QKV) {
-    // QKV row = [Q | K | V], heads 64-contiguous (bert.go:332-347); RoPE on Q and K with
-    // the position = token index (bert.go:349-353, ops_simd.go:127-137).
-    const int D = p.D;
-    const int sec = f / D, fi = f - sec * D, h = fi >> 6, e = fi & 63;
-    const int r = p.tokrow ? p.tokrow[m] : m;
-    const int b = r / p.L, pos = r - b * p.L;
-    if (sec < 2) {
-      const float c0 = o.x, s0 = o.y, c1 = o.z, s1 = o.w;
-      const float a0 = v.x * c0 - v.y * s0, a1 = v.x * s0 + v.y * c0;
-      const float a2 = v.z * c1 - v.w * s1, a3 = v.z * s1 + v.w * c1;
-      __half* dst = (sec == 0 ? p.q : p.k) + (((size_t)b * p.H + h) * p.Lp + pos) * 64 + e;
-      __half2 lo = __floats2half2_rn(a0, a1), hi = __floats2half2_rn(a2, a3);
-      uint2 pk;
-      pk.x = *(uint32_t*)&lo;
-      pk.y = *(uint32_t*)&hi;
-      *(uint2*)dst = pk;
-    } else {
-      __half* dst = p.vt + (((size_t)b * p.H + h) * 64 + e) * p.Lp + pos;
-      dst[0] = __float2half_rn(v.x);
-      dst[(size_t)p.Lp] = __float2half_rn(v.y);
-      dst[(size_t)2 * p.Lp] = __float2half_rn(v.z);
-      dst[(size_t)3 * p.Lp] = __float2half_rn(v.w);
-    }
-  } else {  // EPI_GEGLU: rows interleaved (up q, gate q, up q+1, gate q+1)
-    // gates = GeLU(gate) * up  (internal/embed/bert.go:431-436)
-    const int qo = f >> 1, F = p.N >> 1;
-    const float o0 = gelu_r(v.y) * v.x, o1 = gelu_r(v.w) * v.z;
-    *(__half2*)(p.g + (size_t)m * F + qo) = __floats2half2_rn(o0, o1);
-  }
-}
-
-template <int EPI>
-__device__ __forceinline__ void epilogue(const GemmP& p, int m, int f, floatx4 v) {
-  epilogue_with<EPI>(p, m, f, v, epi_operands<EPI>(p, m, f));
-}
-
-__device__ __forceinline__ uint4 pack8(const float* v) {
-  __half2 a = __floats2half2_rn(v[0], v[1]), b = __floats2half2_rn(v[2], v[3]);
-  __half2 c = __floats2half2_rn(v[4], v[5]), d = __floats2half2_rn(v[6], v[7]);
-  uint4 r;
-  r.x = *(uint32_t*)&a;
-  r.y = *(uint32_t*)&b;
-  r.z = *(uint32_t*)&c;
-  r.w = *(uint32_t*)&d;
-  return r;
-}
-
-__device__ __forceinline__ floatx4 mfma16(const half8& a, const half8& b, const floatx4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// LDS tiles are rows of 16-byte chunks; chunk c of row r is stored at c ^ (r & 7). A wave's
-// ds_read_b128 of 16 rows x one chunk then spreads over all banks (measured on gfx950: 1.8x the
-// read bandwidth of 16-byte-padded rows).
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
-
-// ---------------------------------------------------------------------------------------
-// Canonical chunk of the K reduction: 768 when K is a multiple of 768 (every nomic-bert
-// projection), else 256. Both kernel families derive it from K alone.
-__host__ __device__ constexpr int kchunk_of(int K) { return (K % 768 == 0) ? 768 : 256; }
 
 // Large-M kernel: BM x BN block tile, 4 waves in WM x WN, LDS double buffer over 64-wide K
 // steps, dequantisation at LDS-store time (each weight decoded once per block tile).
@@ -1168,195 +1030,10 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __r
 // straight into LDS for the whole K; block 0 also stores the f32 LayerNorm rows to ln.out.
 template <int FMT, int BM, int BN, int NPIECE, int EPI, bool DIRECT, int LNP = 0>
 __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
-  constexpr int NT = BN * 4, TB = BM / 16, PK = 256;  // one wave per 16 features
-  constexpr int LDW = PK;  // XOR-swizzled chunks (swz)
-  constexpr int WU = BN * (PK / 16);  // segments per piece
-  constexpr int WPT = WU / NT;
-  constexpr int XCH = BM * (PK / 8);
-  constexpr int XPT = (XCH + NT - 1) / NT;
-  constexpr bool AHEAD = FMT != 0;  // f32 weights are too wide to hold every piece in registers
-  constexpr int NP = AHEAD ? NPIECE : 1;
-  constexpr int KF = NPIECE * PK;  // LNP: the whole K
-  // 16-row blocks (the smallest batches, latency-bound) decode every piece into its own LDS
-  // buffer behind one barrier, and the MFMA chain then runs over the whole chunk without stops
-  constexpr bool ALLW = AHEAD && BM == 16;
-  constexpr int NWB = ALLW ? NPIECE : 1;
-  __shared__ __attribute__((aligned(16))) _Float16 sW[NWB][BN][LDW];
-  __shared__ __attribute__((aligned(16))) _Float16 sX[LNP ? 1 : NWB][LNP ? 1 : BM][LDW];
-  __shared__ __attribute__((aligned(16))) _Float16 sXf[LNP ? BM : 1][LNP ? KF : 8];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * BN, c = blockIdx.y, kbase = c * NPIECE * PK;
-  const int mb = blockIdx.z * BM;  // row block (gridDim.z > 1 for 64 < M < 1024)
-  const int M = p.M, K = p.K;
-
-  RawSeg wr[NP][WPT];
-  uint4 xr[NP][XPT];
-  auto load_piece = [&](int slot, int kb) {
-#pragma unroll
-    for (int i = 0; i < WPT; i++) {
-      const int u = tid + i * NT;
-      wr[slot][i] = load_seg<FMT>(p.w, n0 + (u >> 4), kb + (u & 15) * 16);
-    }
-    if constexpr (LNP == 0) {
-#pragma unroll
-      for (int i = 0; i < XPT; i++) {
-        const int cc = tid + i * NT;
-        if (cc < XCH) {
-          const int row = mb + (cc >> 5), ch = cc & 31;
-          xr[slot][i] = row < M ? *(const uint4*)(p.x + (size_t)row * K + kb + ch * 8) : uint4{0, 0, 0, 0};
-        }
-      }
-    }
-  };
-  // LayerNorm prologue: wave w normalises rows w, w + 4 (and w + 8, w + 12). The inputs of rows
-  // 0..7 (all rows of a batch of <= 8 tokens) and the LayerNorm weights are loaded before the
-  // weight stream: vector loads complete in issue order, so issued after it they could not be
-  // used before the whole stream had arrived, and the LayerNorm would only start then.
-  constexpr int NPART = LNP > 0 ? LNP - 1 : 0, NE = LNP > 0 ? KF / 64 : 1;
-  constexpr int LE = LNP > 0 ? MAXE : 1, LP = NPART > 0 ? NPART : 1;
-  float lw[LE], lb[LE], lx[2][LE], lpv[2][LE][LP];
-  auto ln_load = [&](int r0, float (&x)[2][LE], float (&pv)[2][LE][LP]) {
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int r = r0 + wave + 4 * h;
-      if (r < M) {
-#pragma unroll
-        for (int i = 0; i < NE; i++) {
-          const int j = lane + 64 * i;
-          x[h][i] = p.ln.src[(size_t)r * KF + j];
-#pragma unroll
-          for (int q = 0; q < NPART; q++) pv[h][i][q] = p.ln.part[((size_t)q * M + r) * KF + j];
-        }
-      }
-    }
-  };
-  if constexpr (LNP > 0) {
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-      lw[i] = p.ln.w[lane + 64 * i];
-      lb[i] = p.ln.b[lane + 64 * i];
-    }
-    ln_load(0, lx, lpv);
-  }
-  if constexpr (AHEAD) {
-#pragma unroll
-    for (int pc = 0; pc < NPIECE; pc++) load_piece(pc, kbase + pc * PK);
-  }
-
-  if constexpr (LNP > 0) {
-    static_assert(BM == 16 && DIRECT && KF <= 64 * MAXE && NT == 256, "LayerNorm prologue shape");
-    auto ln_rows = [&](int r0, float (&x)[2][LE], float (&pv)[2][LE][LP]) {
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int r = r0 + wave + 4 * h;
-        if (r < M) {
-          if constexpr (NPART > 0) {  // reduce_resid_ln_kernel's order: x + (0 + p0 + p1 + ...)
-#pragma unroll
-            for (int i = 0; i < NE; i++) {
-              float t = 0.f;
-#pragma unroll
-              for (int q = 0; q < NPART; q++) t += pv[h][i][q];
-              x[h][i] = x[h][i] + t;
-            }
-          }
-          ln_apply_wb(x[h], NE, KF, lw, lb, p.ln.eps);
-          if (blockIdx.x == 0 && blockIdx.y == 0) {
-#pragma unroll
-            for (int i = 0; i < NE; i++) p.ln.out[(size_t)r * KF + lane + 64 * i] = x[h][i];
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < NE; i++) x[h][i] = 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < NE; i++) {
-          const int k = lane + 64 * i;  // chunk k/8 stored at (k/8) ^ (r & 7), as swz
-          sXf[r][(((k >> 3) ^ (r & 7)) << 3) + (k & 7)] = (_Float16)__float2half_rn(x[h][i]);
-        }
-      }
-    };
-    ln_rows(0, lx, lpv);
-    float x8[2][LE], pv8[2][LE][LP];
-    ln_load(8, x8, pv8);  // rows 8..15 (no loads when M <= 8)
-    ln_rows(8, x8, pv8);
-  }
-
-  const int lr = lane & 15, lg = lane >> 4;
-  floatx4 eop[DIRECT ? TB : 1];
-  if constexpr (DIRECT) {
-#pragma unroll
-    for (int j = 0; j < TB; j++)
-      if (mb + j * 16 + lr < M) eop[j] = epi_operands<EPI>(p, mb + j * 16 + lr, n0 + wave * 16 + lg * 4);
-  }
-  floatx4 acc[TB];
-#pragma unroll
-  for (int j = 0; j < TB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  auto mma_piece = [&](int pc, int ws) {
-#pragma unroll
-    for (int ks = 0; ks < PK / 32; ks++) {
-      const half8 af = *(const half8*)&sW[ws][wave * 16 + lr][swz(lr, ks * 4 + lg) * 8];
-#pragma unroll
-      for (int j = 0; j < TB; j++) {
-        half8 bf;
-        if constexpr (LNP > 0)
-          bf = *(const half8*)&sXf[j * 16 + lr][(pc * (PK / 8) + swz(lr, ks * 4 + lg)) * 8];
-        else
-          bf = *(const half8*)&sX[ws][j * 16 + lr][swz(lr, ks * 4 + lg) * 8];
-        acc[j] = mfma16(af, bf, acc[j]);
-      }
-    }
-  };
-#pragma unroll
-  for (int pc = 0; pc < NPIECE; pc++) {
-    const int slot = AHEAD ? pc : 0, ws = ALLW ? pc : 0;
-    const int kb = kbase + pc * PK;
-    if constexpr (!AHEAD) load_piece(0, kb);
-    if (!ALLW && pc > 0) __syncthreads();
-    if constexpr (LNP == 0) {
-#pragma unroll
-      for (int i = 0; i < XPT; i++) {
-        const int cc = tid + i * NT;
-        if (cc < XCH) *(uint4*)&sX[ws][cc >> 5][swz(cc >> 5, cc & 31) * 8] = xr[slot][i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < WPT; i++) {
-      const int u = tid + i * NT, row = u >> 4, sg = u & 15;
-      uint4 lo, hi;
-      decode_seg_h<FMT>(wr[slot][i], kb + sg * 16, lo, hi);
-      *(uint4*)&sW[ws][row][swz(row, 2 * sg) * 8] = lo;
-      *(uint4*)&sW[ws][row][swz(row, 2 * sg + 1) * 8] = hi;
-    }
-    if constexpr (!ALLW) {
-      __syncthreads();
-      mma_piece(pc, 0);
-    }
-  }
-  if constexpr (ALLW) {
-    __syncthreads();
-#pragma unroll
-    for (int pc = 0; pc < NPIECE; pc++) mma_piece(pc, pc);
-  }
-  if constexpr (DIRECT) {
-    // single-chunk K: the total is 0 + this chunk, finished here with the epilogue
-#pragma unroll
-    for (int j = 0; j < TB; j++) {
-      const int m = mb + j * 16 + lr;
-      if (m < M) {
-        floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
-        v += acc[j];
-        epilogue_with<EPI>(p, m, n0 + wave * 16 + lg * 4, v, eop[j]);
-      }
-    }
-  } else {
-    float* part = p.part + (size_t)c * M * p.N;
-#pragma unroll
-    for (int j = 0; j < TB; j++) {
-      const int m = mb + j * 16 + lr;
-      if (m < M) *(floatx4*)(part + (size_t)m * p.N + n0 + wave * 16 + (lane >> 4) * 4) = acc[j];
-    }
-  }
+  using SS = SmallShape<FMT, BM, BN, NPIECE, LNP>;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[SS::LDS];
+  RawSeg wr[SS::NP][SS::WPT];
+  gemm_small_dev<FMT, BM, BN, NPIECE, EPI, DIRECT, LNP, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds, wr);
 }
 
 template <int EPI>

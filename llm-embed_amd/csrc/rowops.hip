@@ -1,64 +1,13 @@
 // Row kernels: embedding gather + LayerNorm, LayerNorm, masked mean-pool + L2 (+ Matryoshka),
 // f32 <-> f16 helpers and the raw-GGUF dequantisation test kernel.
-#include "deq_device.h"
-#include "lle_internal.h"
-#include "row_device.h"
+#include "rowops_device.h"
 
 namespace lle {
 
-// Embedding stage (internal/embed/bert.go:220-249, getEmbedding :290-316):
-// h = deq(token_embd[id]) + deq(token_types[0]), then LayerNorm(token_embd_norm).
-// One wave per token. The wave first issues the loads that do not depend on the token id (the
-// type row and the LayerNorm weights), then copies the token's GGUF row into LDS with whole
-// 16-byte (or 2-byte, for rows of odd 8-byte length) loads, and dequantises from there: the
-// per-element scale and code loads of a raw row would otherwise be a dependent global round
-// trip each.
 template <int TY>
 __global__ __launch_bounds__(256) void embed_ln_kernel(EmbedArgs a) {
-  constexpr int RB = 4 * 64 * MAXE;  // bytes of the widest row on the path (F32 at the largest d_model)
-  __shared__ __attribute__((aligned(16))) uint8_t srow[4][RB];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wv;
-  if (t >= a.T) return;  // wave-uniform; the LDS row below is this wave's alone
-  const int ne = a.D / 64;
-  float ty[MAXE], lw[MAXE], lb[MAXE];
-#pragma unroll
-  for (int i = 0; i < MAXE; i++)
-    if (i < ne) {
-      const int j = lane + 64 * i;
-      ty[i] = a.type0[j];
-      lw[i] = a.w[j];
-      lb[i] = a.b[j];
-    }
-  int id = a.ids[t];
-  if (id < 0 || id >= a.vocab) {
-    if (lane == 0) atomicOr(a.status, 1);
-    id = 0;
-  }
-  const uint8_t* row = a.tok + (size_t)id * a.tok_row_bytes;
-  const int nb = (int)a.tok_row_bytes;
-  if ((nb & 15) == 0 && (((uintptr_t)row) & 15) == 0) {
-    for (int o = lane * 16; o < nb; o += 64 * 16) *(uint4*)&srow[wv][o] = *(const uint4*)(row + o);
-  } else {
-    for (int o = lane * 2; o < nb; o += 64 * 2) *(uint16_t*)&srow[wv][o] = *(const uint16_t*)(row + o);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float x[MAXE];
-#pragma unroll
-  for (int i = 0; i < MAXE; i++)
-    if (i < ne) x[i] = deq_raw_t<TY>(srow[wv], lane + 64 * i) + ty[i];
-  ln_apply_wb(x, ne, a.D, lw, lb, a.eps);
-  float* hrow = a.h + (size_t)t * a.D;
-  __half* h16row = a.h16 + (size_t)t * a.D;
-#pragma unroll
-  for (int i = 0; i < MAXE; i++)
-    if (i < ne) {
-      const int j = lane + 64 * i;
-      hrow[j] = x[i];
-      h16row[j] = __float2half_rn(x[i]);
-    }
+  __shared__ __attribute__((aligned(16))) unsigned char lds[EMBED_LDS];
+  embed_ln_dev<TY>(a, blockIdx.x, lds);
 }
 
 hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st) {
@@ -145,61 +94,6 @@ hipError_t launch_reduce_resid_ln(const float* part, int nch, int M, int N, cons
   return hipGetLastError();
 }
 
-// MeanPool + L2Normalize (+ Matryoshka truncation and renormalisation):
-// internal/embed/pool.go:8-54, internal/embed/embedder.go:50-68. Rows with mask == 1 are
-// summed in row order in f32 (the reference's order), scaled by float32(1/count); the norm
-// is accumulated in f64. One block per sequence: the kept rows are first compacted (in order)
-// into an LDS list, then each thread sums 4 adjacent columns with 16 row loads in flight.
-constexpr int POOL_MAXL = 8192;
-
-// Ordered compaction of sequence b's kept positions (mask == 1) into rows[]: per-wave ballot +
-// prefix over the 4 waves of a 256-thread block. Returns their count.
-__device__ int pool_compact(const int32_t* __restrict__ mask, int b, int L, int* rows, int* wcount) {
-  const int tid = threadIdx.x;
-  int base = 0;
-  for (int i0 = 0; i0 < L; i0 += 256) {
-    const int i = i0 + tid;
-    const bool keep = i < L && mask[(size_t)b * L + i] == 1;
-    const unsigned long long bal = __ballot(keep);
-    const int lane = tid & 63, wv = tid >> 6;
-    if (lane == 0) wcount[wv] = __popcll(bal);
-    __syncthreads();
-    int off = base;
-    for (int w2 = 0; w2 < wv; w2++) off += wcount[w2];
-    if (keep) rows[off + __popcll(bal & ((1ull << lane) - 1ull))] = i;
-    base += wcount[0] + wcount[1] + wcount[2] + wcount[3];
-    __syncthreads();
-  }
-  return base;
-}
-
-// L2Normalize of the pooled row vals[0..D) over the first n values, twice when truncating
-// (embedder.go:65-68), then min(out_dim, D) values to out.
-__device__ void pool_finish(float* vals, double* red, int D, int out_dim, float* __restrict__ out) {
-  const int tid = threadIdx.x;
-  int n = D;
-  for (int pass = 0; pass < 2; pass++) {
-    double acc = 0.0;
-    for (int j = tid; j < n; j += 256) acc += (double)vals[j] * (double)vals[j];
-    red[tid] = acc;
-    __syncthreads();
-    for (int s2 = 128; s2 > 0; s2 >>= 1) {
-      if (tid < s2) red[tid] += red[tid + s2];
-      __syncthreads();
-    }
-    const double norm = sqrt(red[0]);
-    __syncthreads();
-    if (norm != 0.0) {
-      const float inv = (float)(1.0 / norm);
-      for (int j = tid; j < n; j += 256) vals[j] = vals[j] * inv;
-    }
-    __syncthreads();
-    if (out_dim >= D) break;
-    n = out_dim;
-  }
-  const int od = out_dim < D ? out_dim : D;
-  for (int j = tid; j < od; j += 256) out[j] = vals[j];
-}
 
 __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ mask,
                                                    const int32_t* __restrict__ seq_off, int L, int D, int out_dim,
@@ -249,82 +143,14 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
   pool_finish(vals, red, D, out_dim, out + (size_t)b * (out_dim < D ? out_dim : D));
 }
 
-// The last LayerNorm of a small forward fused with MeanPool + L2Normalize, one block per
-// sequence. Its kept rows are normalised 16 at a time into LDS with reduce_resid_ln_kernel's
-// arithmetic (residual + (0 + chunk partials in order), ln_row's LayerNorm), and added in row
-// order as pool_kernel adds them; the scaling, norm and Matryoshka tail are pool_kernel's. So
-// the output equals reduce_resid_ln_kernel followed by pool_kernel bit for bit, without the
-// LayerNorm rows going through global memory.
-constexpr int RLP_ROWS = 16;
 template <int NCH>
 __global__ __launch_bounds__(256) void reduce_ln_pool_kernel(const float* __restrict__ part, int M, const float* src,
                                                              const float* w, const float* bb, float eps,
                                                              const int32_t* __restrict__ mask,
                                                              const int32_t* __restrict__ seq_off, int L, int D,
                                                              int out_dim, float* __restrict__ out) {
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  __shared__ double red[256];
-  __shared__ __align__(16) float vals[1024];
-  __shared__ int rows[POOL_MAXL];
-  __shared__ int wcount[5];
-  __shared__ __align__(16) float lnrow[RLP_ROWS][1024];
-  const int count = pool_compact(mask, b, L, rows, wcount);
-  const int row0 = seq_off ? seq_off[b] : b * L;
-  const int ne = D / 64, c0 = 4 * tid;
-  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int i0 = 0; i0 < count; i0 += RLP_ROWS) {
-    for (int k = wv; k < RLP_ROWS; k += 4) {  // wave wv: rows i0 + wv, + 4, + 8, + 12
-      if (i0 + k < count) {
-        const int t = row0 + rows[i0 + k];
-        const float* srow = src + (size_t)t * D;
-        float pv[MAXE][NCH], x[MAXE];
-#pragma unroll
-        for (int i = 0; i < MAXE; i++)
-          if (i < ne) {
-            const int j = lane + 64 * i;
-            x[i] = srow[j];
-#pragma unroll
-            for (int c = 0; c < NCH; c++) pv[i][c] = part[((size_t)c * M + t) * D + j];
-          }
-#pragma unroll
-        for (int i = 0; i < MAXE; i++)
-          if (i < ne) {
-            float acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < NCH; c++) acc += pv[i][c];
-            x[i] = x[i] + acc;
-          }
-        ln_apply(x, ne, D, w, bb, eps, lane);
-#pragma unroll
-        for (int i = 0; i < MAXE; i++)
-          if (i < ne) lnrow[k][lane + 64 * i] = x[i];
-      }
-    }
-    __syncthreads();
-    if (c0 < D) {
-      const int nr = count - i0 < RLP_ROWS ? count - i0 : RLP_ROWS;
-      for (int u = 0; u < nr; u++) {
-        const float4 v = *(const float4*)&lnrow[u][c0];
-        s.x += v.x;
-        s.y += v.y;
-        s.z += v.z;
-        s.w += v.w;
-      }
-    }
-    __syncthreads();
-  }
-  if (c0 < D) {
-    if (count != 0) {
-      const float inv = 1.0f / (float)count;
-      s.x *= inv;
-      s.y *= inv;
-      s.z *= inv;
-      s.w *= inv;
-    }
-    *(float4*)(vals + c0) = s;
-  }
-  __syncthreads();
-  pool_finish(vals, red, D, out_dim, out + (size_t)b * (out_dim < D ? out_dim : D));
+  __shared__ __attribute__((aligned(16))) unsigned char lds[RLP_LDS];
+  reduce_ln_pool_dev<NCH>(part, M, src, w, bb, eps, mask, seq_off, L, D, out_dim, out, blockIdx.x, lds);
 }
 
 hipError_t launch_reduce_ln_pool(const float* part, int nch, int M, const float* src, const float* w, const float* b,
