@@ -323,8 +323,12 @@ __device__ __forceinline__ void attention_dev(const AttnArgs& a, int qt, int h, 
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) tmax = fmaxf(tmax, s[i]);
-        m_u = fmaxf(m_u, max_rows(tmax));
-        if constexpr (THR) thr = keep_threshold(m_u);
+        const float m_new = fmaxf(m_u, max_rows(tmax));
+        if constexpr (THR) {
+          // the threshold follows the maximum, which settles after the first few tiles
+          if (__any(m_new != m_u)) thr = keep_threshold(m_new);
+        }
+        m_u = m_new;
         const bool need = m_u > m_ref + kTau;  // always on the first tile (m_ref = -inf)
         if (__any(need)) {
           const float alpha = need ? __builtin_amdgcn_exp2f((m_ref - m_u) * c1) : 1.f;
@@ -344,21 +348,19 @@ __device__ __forceinline__ void attention_dev(const AttnArgs& a, int qt, int h, 
           return fmaf(u, scale, -m_s) >= -10.f;
       };
       float e[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) e[i] = __builtin_amdgcn_exp2f(fmaf(s[i], c1, nb));
       if (__any(!keeps(tmin))) {
         // some query of the wave drops a key of this tile: exp of a dropped key is discarded,
         // and the smallest kept score is taken over the kept keys (for a query that dropped
-        // nothing both are what the branch below computes)
+        // nothing both are what the tile minimum already holds)
         tmin = INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
           const bool keep = keeps(s[i]);
-          const float ex = __builtin_amdgcn_exp2f(fmaf(s[i], c1, nb));
-          e[i] = keep ? ex : 0.f;
+          e[i] = keep ? e[i] : 0.f;
           tmin = fminf(tmin, keep ? s[i] : INFINITY);
         }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) e[i] = __builtin_amdgcn_exp2f(fmaf(s[i], c1, nb));
       }
       smin = fminf(smin, tmin);  // smallest kept score (exact, order-free)
       // P^T fragments: keys 32j + 8g + 0..7
