@@ -504,8 +504,10 @@ template <int BM, int BN, int WM, int WN, int NS, int EPI, bool MULTI>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FB = TN / 16, TB = TM / 16;
-  constexpr int XI = BM / 8 / NW, WI = BN / 8 / NW;  // 1-KB loads per wave per K step
-  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows per wave");
+  // 1-KB loads per wave per K step; with BN = 288 the 36 W row groups are 5 per wave for waves
+  // 0-3 and 4 for waves 4-7
+  constexpr int XI = BM / 8 / NW, WI = (BN / 8 + NW - 1) / NW;
+  static_assert(BM % (8 * NW) == 0 && BN % 8 == 0, "tile rows per wave");
   static_assert(NS == 2 || NS == 3, "stages");
   // NS stages of [BM X rows | BN W rows] x 128 bytes in one LDS array (stage offsets are
   // compile-time constants); after the K loop the array stages the epilogue's tile
@@ -544,7 +546,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   // their accumulators; their cos / sin rows are brought into the stage the last K step leaves
   // free (ROPE_LDS) and read from LDS in the epilogue.
   constexpr bool QKV = EPI == EPI_QKV && !MULTI;
-  constexpr bool ROPE_LDS = QKV && BM == 256 && BN == 256 && NS == 2;
+  constexpr bool ROPE_LDS = QKV && BM == 256 && (BN == 256 || BN == 288) && NS == 2;
+  static_assert((BN / 8) % NW == 0 || NS == 2, "uneven W loads: the vmcnt accounting assumes 2 stages");
   constexpr bool PRE = EPI == EPI_QKV && !ROPE_LDS;
   floatx4 eop[PRE ? FB : 1][PRE ? TB : 1];
   int qb[(PRE || QKV) ? TB : 1], qp[(PRE || QKV) ? TB : 1];
@@ -557,14 +560,18 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
   // loop-invariant byte offsets; the K step advances in the scalar offset. Rows past M re-read
   // row M-1 (they only feed output rows that are never stored).
   const u32x4_sgpr rx = rsrc_words(p.x), rw = rsrc_words(p.w16);
-  int xo[XI], wo[WI];
+  // An uneven W share (BN = 288) keeps one vector offset, the row group's distance in the
+  // scalar offset: rows j * NW * 8 apart have the same swizzle (r & 7), and five vector offsets
+  // beside 144 accumulators spilled.
+  constexpr bool W1 = (BN / 8) % NW != 0;
+  int xo[XI], wo[W1 ? 1 : WI];
 #pragma unroll
   for (int j = 0; j < XI; j++) {
     const int r = (wave + j * NW) * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
     xo[j] = (min(m0 + r, M - 1) * K + c * 8) * 2;
   }
 #pragma unroll
-  for (int j = 0; j < WI; j++) {
+  for (int j = 0; j < (W1 ? 1 : WI); j++) {
     const int r = (wave + j * NW) * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
     wo[j] = ((n0 + r) * K + c * 8) * 2;
   }
@@ -574,7 +581,14 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
 #pragma unroll
     for (int j = 0; j < XI; j++) dma16(rx, &sx[(wave + j * NW) * 8][0], xo[j], kt * KSTEP * 2);
 #pragma unroll
-    for (int j = 0; j < WI; j++) dma16(rw, &sw[(wave + j * NW) * 8][0], wo[j], kt * KSTEP * 2);
+    for (int j = 0; j < WI; j++) {
+      if constexpr (W1) {
+        if (wave + j * NW < BN / 8)  // wave-uniform
+          dma16(rw, &sw[(wave + j * NW) * 8][0], wo[0], (j * NW * 8 * K + kt * KSTEP) * 2);
+      } else {
+        dma16(rw, &sw[(wave + j * NW) * 8][0], wo[j], kt * KSTEP * 2);
+      }
+    }
   };
   const int lr = lane & 15, lg = lane >> 4;
   auto compute = [&](auto S, int kt) {
@@ -1106,6 +1120,15 @@ static hipError_t launch_lnx1(int type, const GemmP& p, hipStream_t st) {
   }
 }
 
+// Compute units of the current device (blocks of one CU each fill the GPU at this count).
+static int num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0)
+    return 256;
+  return n;
+}
+
 template <int FMT, int EPI>
 static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
   if ((int64_t)p.M * p.K * 2 > INT32_MAX) return hipErrorInvalidValue;  // 32-bit buffer offsets
@@ -1124,11 +1147,26 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
       return hipGetLastError();
     }
     if constexpr (EPI == EPI_QKV) {
-      if (!multi && p.N % 256 == 0 && p.D % 256 == 0 && (p.K / KSTEP) % 2 == 0) {
-        // 256 x 256 tiles, 2 stages of 64 KB, RoPE operands staged in LDS after the K loop
-        dim3 grid(p.N / 256, (p.M + 255) / 256);
-        hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
-        return hipGetLastError();
+      // 256 x 256 or 256 x 288 tiles, 2 stages (64 / 68 KB), RoPE operands staged in LDS after the
+      // K loop (the section is decided per 16-feature fragment, so a 288-wide tile may span two).
+      // The width with fewer rounds of tiles on the CUs, weighted by the tile's fill per K step
+      // (256 + BN rows), wins: N = 2304 takes 288 at 8192 tokens (one round against two) and at
+      // 32768 (four against five).
+      if (!multi && (p.K / KSTEP) % 2 == 0 && p.D % 16 == 0) {
+        const int64_t mt = (p.M + 255) / 256, cus = num_cus();
+        auto cost = [&](int bn) { return ((p.N / bn) * mt + cus - 1) / cus * (256 + bn); };
+        const bool w256 = p.N % 256 == 0 && p.D % 256 == 0;
+        dim3 grid(1, (p.M + 255) / 256);
+        if (p.N % 288 == 0 && (!w256 || cost(288) < cost(256))) {
+          grid.x = p.N / 288;
+          hipLaunchKernelGGL((gemm_h<256, 288, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
+          return hipGetLastError();
+        }
+        if (w256) {
+          grid.x = p.N / 256;
+          hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
+          return hipGetLastError();
+        }
       }
     }
     if ((p.K / KSTEP) % 3 == 0) {
@@ -1233,15 +1271,6 @@ hipError_t launch_gemm_lnx(const GemmArgs& a, int epi, const LnPrologue& ln, hip
     case EPI_GEGLU: return launch_lnx1<EPI_GEGLU>(a.w->type, p, st);
     default: return hipErrorInvalidValue;
   }
-}
-
-// Compute units of the current device (blocks of one CU each fill the GPU at this count).
-static int num_cus() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n <= 0)
-    return 256;
-  return n;
 }
 
 hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
