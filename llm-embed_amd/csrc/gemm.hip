@@ -941,6 +941,103 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln(GemmP p, const float* __res
   rowln_finish<BM>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane);
 }
 
+// Epilogue of the LDS-DMA full-row kernel, in 16-token slabs. Slab s's residual rows
+// (16 x 768 f32) are brought into LDS by LDS-DMA (two buffers, row stride LN_RS floats) while
+// the previous slab is normalised, the accumulators are added in place (x = h + (0 + total), as
+// rowln_finish), and each wave normalises two rows with ln_row's arithmetic, so every bit equals
+// rowln_finish's. The waits count this wave's younger memory operations exactly: slab s + 1's six
+// DMA instructions and the 24 stores of each of its two rows of slab s - 1 (a skipped row past M
+// stores nothing, which only makes the wait stricter).
+template <int BM>
+__device__ __forceinline__ void rowln_finish_dma(const floatx4 (&acc)[6][BM / 16], unsigned char* smem, const GemmP& p,
+                                                 const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                                 float eps, __half* h16, int m0, int wn, int lane) {
+  constexpr int FB = 6, TN = 96, NE = LN_N / 64, NSL = BM / 16;
+  constexpr int SLAB = 16 * LN_RS * 4;  // bytes of one slab buffer
+  constexpr int DMA_PER = 6;             // 48 KB-instructions per slab over 8 waves
+  constexpr int ST = 2 * 2 * NE;         // stores per lane per slab: two rows, f32 + f16 each
+  static_assert(NE == 12 && DMA_PER + ST < 64, "vmcnt range");
+  const int lr = lane & 15, lg = lane >> 4, M = p.M;
+  const u32x4_sgpr ry = rsrc_words(p.y);
+  auto slab = [&](int s) { return (float*)(smem + (s & 1) * SLAB); };
+  // instruction t of wave w moves the 1 KB part (6w + t) % 3 of slab row (6w + t) / 3 (rows
+  // past M read row M - 1: they are never stored)
+  auto dma_slab = [&](int s) {
+    float* buf = slab(s);
+#pragma unroll
+    for (int t = 0; t < DMA_PER; t++) {
+      const int idx = wn * DMA_PER + t, row = idx / 3, part = idx - row * 3;
+      const int m = min(m0 + s * 16 + row, M - 1);
+      dma16(ry, buf + row * LN_RS + part * 256, lane * 16, (m * LN_N + part * 256) * 4);
+    }
+  };
+  auto wait_bar = [&](auto VMC) {
+    constexpr int V = decltype(VMC)::value;
+    __builtin_amdgcn_s_waitcnt((V & 0xF) | ((V >> 4) << 14) | (0x7 << 4));  // vmcnt(V) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // the LayerNorm weights and biases come into LDS with slab 0 (waves 0-5, one 1 KB part
+  // each), so the epilogue has no global loads the compiler's wait counting would have to order
+  // against the DMA
+  float* sWB = (float*)(smem + 2 * SLAB);
+  float wv[MAXE], bv[MAXE];
+  dma_slab(0);
+  if (wn < 6) {
+    const int part = wn % 3;
+    dma16(rsrc_words(wn < 3 ? lnw : lnb), sWB + (wn / 3) * LN_N + part * 256, lane * 16, part * 1024);
+  }
+#pragma unroll
+  for (int s = 0; s < NSL; s++) {
+    if (s + 1 < NSL) dma_slab(s + 1);  // its buffer was last read before the previous barrier
+    if (s == 0)
+      wait_bar(std::integral_constant<int, DMA_PER>{});
+    else if (s + 1 < NSL)
+      wait_bar(std::integral_constant<int, DMA_PER + ST>{});
+    else
+      wait_bar(std::integral_constant<int, ST>{});
+    float* buf = slab(s);
+#pragma unroll
+    for (int i = 0; i < FB; i++) {
+      float* px = buf + lr * LN_RS + wn * TN + i * 16 + lg * 4;
+      floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+      v += acc[i][s];  // total = 0 + chunk
+      const floatx4 h = *(const floatx4*)px;
+      floatx4 x;
+      x.x = h.x + v.x; x.y = h.y + v.y; x.z = h.z + v.z; x.w = h.w + v.w;
+      *(floatx4*)px = x;
+    }
+    wait_bar(std::integral_constant<int, 63>{});  // LDS only
+    if (s == 0) {
+#pragma unroll
+      for (int i = 0; i < NE; i++) {
+        wv[i] = sWB[lane + 64 * i];
+        bv[i] = sWB[LN_N + lane + 64 * i];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int tl = wn * 2 + r, m = m0 + s * 16 + tl;
+      if (m < M) {
+        float x[MAXE];
+#pragma unroll
+        for (int i = 0; i < MAXE; i++)
+          if (i < NE) x[i] = buf[tl * LN_RS + lane + 64 * i];
+        ln_apply_wb(x, NE, LN_N, wv, bv, eps);
+        float* hrow = p.y + (size_t)m * LN_N;
+        __half* h16row = h16 + (size_t)m * LN_N;
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+          hrow[lane + 64 * i] = x[i];
+          h16row[lane + 64 * i] = __float2half_rn(x[i]);
+        }
+      }
+    }
+    if (s + 1 < NSL) wait_bar(std::integral_constant<int, 63>{});  // buffer s & 1 read by all
+  }
+}
+
 // The full-row kernel on the resident f16 weights: both tiles by LDS-DMA (one instruction =
 // 16 rows of 64 bytes; lane L fills slot L % 4 of row L / 4 with logical chunk (L % 4) ^ swr(row))
 // through NS LDS stages (3 x 52 KB for 64 rows, 2 x 56 KB for 128), loads NS - 1 K steps ahead;
@@ -957,6 +1054,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __r
   constexpr int R_BYTES = 32 * LN_RS * 4;
   constexpr int SMEM = NS * STAGE > R_BYTES ? NS * STAGE : R_BYTES;
   static_assert(SMEM <= 160 * 1024, "LDS");
+  static_assert(SMEM >= 2 * 16 * LN_RS * 4 + 2 * LN_N * 4, "LDS of the epilogue's slabs and weights");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
   typedef _Float16 Row[LN_KS];
 
@@ -1031,7 +1129,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __r
     stage = stage == NS - 1 ? 0 : stage + 1;
   }
   __syncthreads();  // every stage read: LDS is free for the row staging
-  rowln_finish<BM>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane);
+  rowln_finish_dma<BM>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane);
 }
 
 // ---------------------------------------------------------------------------------------
