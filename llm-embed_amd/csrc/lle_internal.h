@@ -143,8 +143,9 @@ struct AttnArgs {
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 
+// scratch (B x D floats, may be null): the per-sequence means of the sliced form for few long rows
 hipError_t launch_pool(const float* h, const int32_t* mask, const int32_t* seq_off, int B, int L, int D, int out_dim,
-                       float* out, hipStream_t st);
+                       float* out, float* scratch, size_t scratch_bytes, hipStream_t st);
 // launch_reduce_resid_ln (rows of N = D, nch = 4) followed by launch_pool, in one kernel that
 // keeps the LayerNorm rows in LDS; bit-identical to the two kernels. The LayerNorm rows are not
 // stored.

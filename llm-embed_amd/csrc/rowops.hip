@@ -207,9 +207,102 @@ hipError_t launch_pack_tables(const int32_t* in_off, int B, int T, int L, int32_
   return hipGetLastError();
 }
 
+// Mean-pool of few long sequences: one block per (sequence, 64-column slice), so a sequence's
+// rows are read by D / 64 CUs instead of one. Each column is summed over the kept rows in row
+// order in f32 and scaled by 1 / count, exactly as pool_kernel does it, so the bits are the same.
+// The 4 waves bring 64-row chunks into a 6-buffer LDS ring by LDS-DMA five chunks ahead (one
+// 1 KB instruction = 4 rows x 256 bytes, gathered through the kept-row list); wave 0 adds them
+// (lane = column). The scaled slice goes to vals[b][D]; pool_norm_kernel finishes each row.
+typedef __attribute__((address_space(3))) void* pool_lds_t;
+typedef unsigned int pool_rsrc_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void pool_dma16(pool_rsrc_t r, void* lds, int voff) {
+  const uint32_t base = (uint32_t)(uintptr_t)(pool_lds_t)lds;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(base), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+constexpr int PSL_CH = 64, PSL_NB = 6;  // rows per chunk, LDS buffers
+__global__ __launch_bounds__(256) void pool_slice_kernel(const float* __restrict__ h, const int32_t* __restrict__ mask,
+                                                         const int32_t* __restrict__ seq_off, int L, int D,
+                                                         float* __restrict__ vals) {
+  __shared__ int rows[POOL_MAXL];
+  __shared__ int wcount[5];
+  __shared__ __attribute__((aligned(1024))) float buf[PSL_NB][PSL_CH][64];
+  const int b = blockIdx.x, col = blockIdx.y * 64, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int count = pool_compact(mask, b, L, rows, wcount);
+  const float* hb = h + (size_t)(seq_off ? seq_off[b] : b * L) * D + col;
+  const uint64_t a = (uint64_t)(uintptr_t)hb;
+  const pool_rsrc_t rs = pool_rsrc_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, 0xffffffffu, 0x00020000u};
+  const int nch = (count + PSL_CH - 1) / PSL_CH;
+  // chunk c, instruction k of wave w: chunk rows w * 16 + 4 k + lane / 16, 16 bytes (lane % 16);
+  // rows past the last kept one re-read it (never added)
+  auto issue = [&](int c) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int i = min(c * PSL_CH + wave * 16 + 4 * k + (lane >> 4), count - 1);
+      pool_dma16(rs, &buf[c % PSL_NB][wave * 16 + 4 * k][0], (rows[i] * D + (lane & 15) * 4) * 4);
+    }
+  };
+  for (int c = 0; c < PSL_NB - 1 && c < nch; c++) issue(c);
+  float s = 0.f;
+  for (int c = 0; c < nch; c++) {
+    // this wave's loads of chunk c have landed once only those of the (up to PSL_NB - 2)
+    // younger chunks issued so far are in flight (4 instructions each)
+    switch (min(nch - 1 - c, PSL_NB - 2)) {
+      case 4: __builtin_amdgcn_s_waitcnt(16 & 0xF | (16 >> 4) << 14 | 0x7 << 4); break;  // vmcnt(16) lgkmcnt(0)
+      case 3: __builtin_amdgcn_s_waitcnt(12 | 0x7 << 4); break;
+      case 2: __builtin_amdgcn_s_waitcnt(8 | 0x7 << 4); break;
+      case 1: __builtin_amdgcn_s_waitcnt(4 | 0x7 << 4); break;
+      default: __builtin_amdgcn_s_waitcnt(0x7 << 4); break;
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (c + PSL_NB - 1 < nch) issue(c + PSL_NB - 1);  // into chunk c - 1's buffer, read before the barrier
+    if (wave == 0) {
+      const int n = min(PSL_CH, count - c * PSL_CH);
+      const float* bc = &buf[c % PSL_NB][0][lane];
+      int r = 0;
+      for (; r + 16 <= n; r += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = bc[(r + u) * 64];
+#pragma unroll
+        for (int u = 0; u < 16; u++) s += v[u];
+      }
+      for (; r < n; r++) s += bc[r * 64];
+    }
+  }
+  if (wave == 0) {
+    if (count != 0) s *= 1.0f / (float)count;
+    vals[(size_t)b * D + col + lane] = s;
+  }
+}
+
+__global__ __launch_bounds__(256) void pool_norm_kernel(const float* __restrict__ vals, int D, int out_dim,
+                                                        float* __restrict__ out) {
+  __shared__ double red[256];
+  __shared__ __align__(16) float v[1024];
+  const int b = blockIdx.x;
+  for (int j = threadIdx.x; j < D; j += 256) v[j] = vals[(size_t)b * D + j];
+  __syncthreads();
+  pool_finish(v, red, D, out_dim, out + (size_t)b * (out_dim < D ? out_dim : D));
+}
+
 hipError_t launch_pool(const float* h, const int32_t* mask, const int32_t* seq_off, int B, int L, int D, int out_dim,
-                       float* out, hipStream_t st) {
+                       float* out, float* scratch, size_t scratch_bytes, hipStream_t st) {
   if (L > POOL_MAXL || D > 1024 || D % 4) return hipErrorInvalidValue;
+  // The sliced form when one block per sequence would leave most CUs idle on long rows
+  // (config 5: 8 sequences of 1024-2048 rows, 84 us in pool_kernel).
+  if (B <= 64 && L >= 512 && D % 64 == 0 && scratch && scratch_bytes >= (size_t)B * D * 4) {
+    hipLaunchKernelGGL(pool_slice_kernel, dim3(B, D / 64), dim3(256), 0, st, h, mask, seq_off, L, D, scratch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(pool_norm_kernel, dim3(B), dim3(256), 0, st, scratch, D, out_dim, out);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(pool_kernel, dim3(B), dim3(256), 0, st, h, mask, seq_off, L, D, out_dim, out);
   return hipGetLastError();
 }

@@ -561,7 +561,8 @@ static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const
   }
   if (d_out) {
     Scope s(m, st, "pool", 0, (double)T * D * 4, timed);
-    LAUNCH(launch_pool(w.h, d_mask, seq_off, B, L, D, out_dim, d_out, st));
+    // the FFN buffer is free by now: it holds the sliced pool's per-sequence means
+    LAUNCH(launch_pool(w.h, d_mask, seq_off, B, L, D, out_dim, d_out, (float*)w.ff, (size_t)T * F * 2, st));
   }
   return LLE_OK;
 }

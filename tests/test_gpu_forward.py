@@ -299,6 +299,32 @@ def test_long_sequence(gpu, small_spec):
         compare(e.embed(ids), o.embed(ids), f"long L={L}")
 
 
+def test_sliced_pool_bitexact(gpu, small_spec):
+    """Few long rows (B <= 64, padded L >= 512) are mean-pooled by D/64 column-slice blocks,
+    other batches by one block per sequence (and <= 64 tokens inside the last LayerNorm kernel).
+    Every form sums each column over the kept rows in row order, so a sequence's embedding has
+    the same bits whichever form pools it: lengths on both sides of the rule embedded alone,
+    padded together to L = 1100 (sliced), and in a batch of 68 rows of that length (row form)."""
+    e, o = models(small_spec, "Q8_0")
+    rng = np.random.default_rng(14)
+    lens = [300, 513, 40, 1000]
+    seqs = [rng.integers(0, small_spec.vocab, n).astype(np.int32) for n in lens]
+    alone = [e.embed(s) for s in seqs]
+    L = 1100
+    ids = np.zeros((len(lens), L), np.int32)
+    mask = np.zeros((len(lens), L), np.int32)
+    for i, s in enumerate(seqs):
+        ids[i, : len(s)] = s
+        mask[i, : len(s)] = 1
+    batch = e.embed_padded(ids, mask)
+    many = e.embed_padded(np.tile(ids, (17, 1)), np.tile(mask, (17, 1)))
+    for i in range(len(lens)):
+        assert np.array_equal(bits(batch[i]), bits(alone[i])), lens[i]
+        assert np.array_equal(bits(many[i]), bits(alone[i])), lens[i]
+        assert np.array_equal(bits(many[4 * 16 + i]), bits(alone[i])), lens[i]
+    compare(batch[1], o.embed(seqs[1]), "sliced pool L=513")
+
+
 def test_errors(gpu, small_spec):
     e, _ = models(small_spec, "Q8_0")
     with pytest.raises(LLEError):
