@@ -722,7 +722,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     // (32 lanes per 512-byte row) instead of 16 rows x 64 bytes per instruction.
     typedef float TRow[128];
     static_assert(sizeof(smem) >= 256 * sizeof(TRow), "staging");
-    __syncthreads();  // every wave is done reading the last stage
+    // all 16 residual chunks of this thread are loaded first (rows past M: the last row, never
+    // stored), so their one round trip overlaps the staging; the barriers below wait for LDS
+    // only and leave them in flight
+    const int N = p.N;
+    floatx4 res[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const int q = tid + k * 512, row = q >> 5, c = q & 31;
+      res[k] = *(const floatx4*)(p.y + (size_t)min(m0 + row, M - 1) * N + n0 + c * 4);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every wave is done reading the last stage
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     TRow* so = (TRow*)smem;
 #pragma unroll
     for (int j = 0; j < TB; j++) {
@@ -739,26 +752,18 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
         *(floatx4*)&so[r][((wn * 16 + i * 4 + lg) ^ (r & 31)) * 4] = v;
       }
     }
-    __syncthreads();
-    const int N = p.N;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int k0 = 0; k0 < 16; k0 += 8) {
-      floatx4 res[8];
-#pragma unroll
-      for (int k = 0; k < 8; k++) {  // residual loads first: one round trip for 8 chunks
-        const int q = tid + (k0 + k) * 512, row = q >> 5, c = q & 31;
-        res[k] = m0 + row < M ? *(const floatx4*)(p.y + (size_t)(m0 + row) * N + n0 + c * 4)
-                              : floatx4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const int q = tid + (k0 + k) * 512, row = q >> 5, c = q & 31;
-        const floatx4 v = *(const floatx4*)&so[row][(c ^ (row & 31)) * 4];
-        // hiddens[i][j] += out[i][j]  (internal/embed/bert.go:262-264, 276-278)
-        floatx4 h = res[k];
-        h.x = h.x + v.x; h.y = h.y + v.y; h.z = h.z + v.z; h.w = h.w + v.w;
-        if (m0 + row < M) *(floatx4*)(p.y + (size_t)(m0 + row) * N + n0 + c * 4) = h;
-      }
+    for (int k = 0; k < 16; k++) {
+      const int q = tid + k * 512, row = q >> 5, c = q & 31;
+      const floatx4 v = *(const floatx4*)&so[row][(c ^ (row & 31)) * 4];
+      // hiddens[i][j] += out[i][j]  (internal/embed/bert.go:262-264, 276-278)
+      floatx4 h = res[k];
+      h.x = h.x + v.x; h.y = h.y + v.y; h.z = h.z + v.z; h.w = h.w + v.w;
+      if (m0 + row < M) *(floatx4*)(p.y + (size_t)(m0 + row) * N + n0 + c * 4) = h;
     }
     return;
   }
