@@ -712,7 +712,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     for (int k = 0; k < 8; k++) {
       const int q = tid + k * 512, row = q >> 4, c = q & 15, rr = row & 127;
       const uint4 val = *(const uint4*)&((const ORow*)smem)[row][(c ^ (rr & 15)) * 8];
-      if (m0 + row < M) *(uint4*)(p.g + (size_t)(m0 + row) * F + (n0 >> 1) + c * 8) = val;
+      if (m0 + row < M)  // streaming store: measured faster than a cached one for this 200 MB output
+        __builtin_nontemporal_store(u32x4_sgpr{val.x, val.y, val.z, val.w},
+                                    (u32x4_sgpr*)(p.g + (size_t)(m0 + row) * F + (n0 >> 1) + c * 8));
     }
     return;
   }
@@ -763,7 +765,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
       // hiddens[i][j] += out[i][j]  (internal/embed/bert.go:262-264, 276-278)
       floatx4 h = res[k];
       h.x = h.x + v.x; h.y = h.y + v.y; h.z = h.z + v.z; h.w = h.w + v.w;
-      if (m0 + row < M) *(floatx4*)(p.y + (size_t)(m0 + row) * N + n0 + c * 4) = h;
+      if (m0 + row < M) __builtin_nontemporal_store(h, (floatx4*)(p.y + (size_t)(m0 + row) * N + n0 + c * 4));
     }
     return;
   }
