@@ -412,6 +412,28 @@ def test_packed_rows_equal_padded_forward(gpu, small_spec, B, L, seed):
     compare(host[1:], o.embed_batch(ids[1:], mask[1:]), f"packed B={B} L={L}")
 
 
+@pytest.mark.parametrize("B,last", [(188, 64), (260, 37)])
+def test_ragged_large_batch_tiles(gpu, small_spec, B, last):
+    """Packed row counts that leave the large-batch tiles partly past the last row: 24,000 rows
+    (256 x 288 QKV tiles, the last 256-row tile 64 rows short) and 33,189 rows (the 128-row
+    full-row out projection's last block 91 rows short, and partial last 256-row tiles of the
+    down and up||gate GEMMs). Rows of sequences at the start, middle and end of the batch equal the same
+    sequences embedded alone bit for bit, and match the oracle."""
+    e, o = models(small_spec, "Q8_0")
+    L = 128
+    rng = np.random.default_rng(B)
+    ids = rng.integers(0, small_spec.vocab, (B, L)).astype(np.int32)
+    mask = np.ones((B, L), np.int32)
+    mask[-1, last:] = 0
+    print(f"ragged: B={B} rows {int(mask.sum())}", flush=True)
+    batch = e.embed_padded(ids, mask)
+    assert np.all(np.isfinite(batch))
+    for i in (0, B // 2, B - 2, B - 1):
+        n = int(mask[i].sum())
+        assert np.array_equal(bits(e.embed(ids[i, :n])), bits(batch[i])), i
+    compare(batch[[0, B - 1]], o.embed_batch(ids[[0, B - 1]], mask[[0, B - 1]]), f"ragged B={B}")
+
+
 def test_key_tile_boundaries(gpu, small_spec):
     """Sequences whose last stored key falls exactly on, just past, and well inside a 64-key
     tile (lengths 64, 128, 65, 192 and 1 in a batch padded to 192): the attention reads K tiles
