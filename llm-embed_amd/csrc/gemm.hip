@@ -718,19 +718,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     }
     return;
   }
-  if constexpr (EPI == EPI_RESID && BM == 256 && BN == 128 && WM == 4 && WN == 2) {
+  if constexpr (EPI == EPI_RESID && (BM == 256 || BM == 128) && BN == 128 && WM == 4 && WN == 2) {
     // h += X W^T through LDS: the f32 tile totals are staged (row r's 16-byte chunk c at
     // c ^ (r & 31)), then each thread reads 16 bytes of residual, adds and stores whole row chunks
     // (32 lanes per 512-byte row) instead of 16 rows x 64 bytes per instruction.
     typedef float TRow[128];
-    static_assert(sizeof(smem) >= 256 * sizeof(TRow), "staging");
-    // all 16 residual chunks of this thread are loaded first (rows past M: the last row, never
-    // stored), so their one round trip overlaps the staging; the barriers below wait for LDS
-    // only and leave them in flight
+    static_assert(sizeof(smem) >= BM * sizeof(TRow), "staging");
+    // all BM / 16 residual chunks of this thread are loaded first (rows past M: the last row,
+    // never stored), so their one round trip overlaps the staging; the barriers below wait for
+    // LDS only and leave them in flight
     const int N = p.N;
-    floatx4 res[16];
+    constexpr int RC = BM / 16;
+    floatx4 res[RC];
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
+    for (int k = 0; k < RC; k++) {
       const int q = tid + k * 512, row = q >> 5, c = q & 31;
       res[k] = *(const floatx4*)(p.y + (size_t)min(m0 + row, M - 1) * N + n0 + c * 4);
     }
@@ -741,7 +742,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     TRow* so = (TRow*)smem;
 #pragma unroll
     for (int j = 0; j < TB; j++) {
-      const int r = wm * 64 + j * 16 + lr;
+      const int r = wm * TM + j * 16 + lr;
 #pragma unroll
       for (int i = 0; i < FB; i++) {
         floatx4 v;
@@ -759,7 +760,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_h(GemmP p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
+    for (int k = 0; k < RC; k++) {
       const int q = tid + k * 512, row = q >> 5, c = q & 31;
       const floatx4 v = *(const floatx4*)&so[row][(c ^ (row & 31)) * 4];
       // hiddens[i][j] += out[i][j]  (internal/embed/bert.go:262-264, 276-278)
@@ -1270,6 +1271,23 @@ static hipError_t launch_fmt(const GemmP& p, hipStream_t st, bool reduce) {
         if (w256) {
           grid.x = p.N / 256;
           hipLaunchKernelGGL((gemm_h<256, 256, 4, 2, 2, EPI, false>), grid, dim3(512), 0, st, p);
+          return hipGetLastError();
+        }
+      }
+    }
+    if constexpr (EPI == EPI_RESID) {
+      // 128-row tiles (3 stages of 32 KB) when they take fewer rounds of the CUs, weighted by
+      // the fill per K step (BM + 128 rows): mid-size batches (e.g. 5017 rows: 240 blocks
+      // instead of 120) keep every CU busy
+      if ((p.K / KSTEP) % 3 == 0 && p.N % 128 == 0) {
+        const int64_t cus = num_cus(), nt = p.N / 128;
+        auto cost = [&](int bm) { return ((p.M + bm - 1) / bm * nt + cus - 1) / cus * (bm + 128); };
+        if (cost(128) < cost(256)) {
+          dim3 grid(p.N / 128, (p.M + 127) / 128);
+          if (multi)
+            hipLaunchKernelGGL((gemm_h<128, 128, 4, 2, 3, EPI, true>), grid, dim3(512), 0, st, p);
+          else
+            hipLaunchKernelGGL((gemm_h<128, 128, 4, 2, 3, EPI, false>), grid, dim3(512), 0, st, p);
           return hipGetLastError();
         }
       }
