@@ -29,7 +29,9 @@ namespace lle {
 template <int NW, bool EARLY>
 __global__ __launch_bounds__(NW * 64, NW == 8 ? 4 : 1) void attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[AttnShape<NW>::LDS];
-  attention_dev<NW, EARLY>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  // workgroup ids by the compiler builtins (see attention_dev's thread id)
+  attention_dev<NW, EARLY>(a, __builtin_amdgcn_workgroup_id_x(), __builtin_amdgcn_workgroup_id_y(),
+                           __builtin_amdgcn_workgroup_id_z(), lds);
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {

@@ -101,7 +101,10 @@ __device__ __forceinline__ void attention_dev(const AttnArgs& a, int qt, int h, 
   int* sFull = reinterpret_cast<int*>(lds + AS::FULL);
   int& sRedo = *reinterpret_cast<int*>(lds + AS::REDO);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the compiler builtin, not threadIdx.x: this file is built with the IEEE-mode bit off, so
+  // the device library's index functions (built with it on) are not inlined but called, and
+  // every call waits for all outstanding loads first
+  const int tid = __builtin_amdgcn_workitem_id_x(), lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, lr = lane & 15;
   const int L = a.L, Lp = a.Lp, H = a.H;
   const size_t head = (size_t)b * H + h;
@@ -112,7 +115,9 @@ __device__ __forceinline__ void attention_dev(const AttnArgs& a, int qt, int h, 
   const size_t orow = a.seq_off ? (size_t)a.seq_off[b] : (size_t)b * L;
   // only valid (mask 1) queries may ask for the fixed-max pass: padding queries' outputs are
   // never used, and the pass decision must not depend on how a sequence was padded
-  const bool qvalid = q < L && a.mask[(size_t)b * L + q] == 1;
+  // (loaded here for every lane, clamped, and tested only after the pass: a conditional load
+  // here made the compiler wait for it at once)
+  const int qmask = a.mask[(size_t)b * L + min(q, L - 1)];
 
   // Q^T fragments (B operand of S): query q, dims ks*32 + 8g .. +7
   half8 qf[2];
@@ -175,9 +180,10 @@ __device__ __forceinline__ void attention_dev(const AttnArgs& a, int qt, int h, 
     const int32_t* mrow = a.mask + (size_t)b * L;
     int lo = L, hi = -1, i0 = tid;
     if constexpr (EARLY) {
-      const int mv0 = tid < L ? mrow[tid] : 0;
+      const int mv0 = mrow[min(tid, L - 1)];  // unconditional: a guarded load was waited for at once
       gload(0);
-      if (mv0 != 0) {
+      __builtin_amdgcn_sched_barrier(0);  // the tile's loads are issued before the test waits
+      if (tid < L && mv0 != 0) {
         lo = tid;
         hi = tid;
       }
@@ -392,6 +398,7 @@ __device__ __forceinline__ void attention_dev(const AttnArgs& a, int qt, int h, 
     }
     if (!fixed) {
       const float sm = min_rows(smin) * scale;
+      const bool qvalid = q < L && qmask == 1;
       const bool flag = qvalid && (sm - m_u * scale < -10.f);
       if (__any(flag)) sRedo = 1;  // benign race: every writer stores 1
     }
