@@ -162,7 +162,9 @@ struct SmallShape {
   // buffer behind one barrier, and the MFMA chain then runs over the whole chunk without stops
   static constexpr bool ALLW = AHEAD && BM == 16;
   static constexpr int NWB = ALLW ? NPIECE : 1;
-  static constexpr size_t SW = (size_t)NWB * BN * LDW * 2;
+  // weight staging; with a LayerNorm prologue it first holds the prologue's 16 rows + w, b (f32)
+  static constexpr size_t SWW = (size_t)NWB * BN * LDW * 2, SLN = LNP ? (size_t)(16 + 2) * KF * 4 : 0;
+  static constexpr size_t SW = SWW > SLN ? SWW : SLN;
   static constexpr size_t SX = (size_t)(LNP ? 1 : NWB) * (LNP ? 1 : BM) * LDW * 2;
   static constexpr size_t SXF = (size_t)(LNP ? BM : 1) * (LNP ? KF : 8) * 2;
   static constexpr size_t LDS = SW + SX + SXF;  // bytes, every part a multiple of 16
@@ -230,35 +232,60 @@ __device__ __forceinline__ void gemm_small_dev(const GemmP& p, int bx, int by, i
       }
     }
   };
-  // LayerNorm prologue: wave w normalises rows w, w + 4 (and w + 8, w + 12). The inputs of rows
-  // 0..7 (all rows of a batch of <= 8 tokens) and the LayerNorm weights are loaded before the
-  // weight stream: vector loads complete in issue order, so issued after it they could not be
-  // used before the whole stream had arrived, and the LayerNorm would only start then.
+  // LayerNorm prologue: wave w normalises rows w, w + 4 (and w + 8, w + 12). Its inputs (the
+  // residual rows, the partial chunks to add to them, the LayerNorm weights) are read with
+  // 16-byte loads, 4 consecutive elements per lane, and summed element by element in
+  // reduce_resid_ln_kernel's order, x + (0 + p0 + p1 + ...): 32 loads per lane for rows 0..7 and
+  // the weights, so that with the weight stream (24) every load is in flight at once (a wave can
+  // have 63; 144 four-byte loads made it wait for the first ones before issuing the weights).
+  // The sums go through LDS, the weight staging area, which is free until the pieces are decoded,
+  // into ln_row's element-to-lane mapping (element lane + 64 i), so the LayerNorm's arithmetic and
+  // every output bit are unchanged. The inputs of rows 0..7 are loaded before the weight stream:
+  // vector loads complete in issue order, so issued after it they could not be used before the
+  // whole stream had arrived.
   constexpr int NPART = LNP > 0 ? LNP - 1 : 0, NE = LNP > 0 ? KF / 64 : 1;
-  constexpr int LE = LNP > 0 ? MAXE : 1, LP = NPART > 0 ? NPART : 1;
-  float lw[LE], lb[LE], lx[2][LE], lpv[2][LE][LP];
-  auto ln_load = [&](int r0, float (&x)[2][LE], float (&pv)[2][LE][LP]) {
+  constexpr int G = LNP > 0 ? KF / 256 : 1;  // 16-byte groups per lane and row
+  static_assert(LNP == 0 || (KF % 256 == 0 && (16 + 2) * KF * 4 <= SS::SW), "prologue staging");
+  float* stg = reinterpret_cast<float*>(lds);  // rows [16][KF], then w and b [2][KF]
+  constexpr int NPQ = NPART > 0 ? NPART : 1;
+  floatx4 xs[2][G], pv[2][G][NPQ], wb4[2];  // native vectors: HIP's float4 struct kept these in memory
+  // loads only (rows past M re-read row M - 1 and are not used): the sums come after the weight
+  // stream is issued, so that no wait sits between these loads and it
+  auto ln_issue = [&](int r0) {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const int r = r0 + wave + 4 * h;
-      if (r < M) {
+      const int r = min(r0 + wave + 4 * h, M - 1);
 #pragma unroll
-        for (int i = 0; i < NE; i++) {
-          const int j = lane + 64 * i;
-          x[h][i] = p.ln.src[(size_t)r * KF + j];
+      for (int g = 0; g < G; g++) {
+        const int j = g * 256 + lane * 4;
+        xs[h][g] = *(const floatx4*)(p.ln.src + (size_t)r * KF + j);
 #pragma unroll
-          for (int q = 0; q < NPART; q++) pv[h][i][q] = p.ln.part[((size_t)q * M + r) * KF + j];
-        }
+        for (int q = 0; q < NPART; q++) pv[h][g][q] = *(const floatx4*)(p.ln.part + ((size_t)q * M + r) * KF + j);
       }
     }
   };
-  if constexpr (LNP > 0) {
+  auto ln_sum = [&]() {
+    if constexpr (NPART > 0) {
 #pragma unroll
-    for (int i = 0; i < NE; i++) {
-      lw[i] = p.ln.w[lane + 64 * i];
-      lb[i] = p.ln.b[lane + 64 * i];
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+          floatx4 t = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int q = 0; q < NPART; q++) {
+            t.x += pv[h][g][q].x; t.y += pv[h][g][q].y; t.z += pv[h][g][q].z; t.w += pv[h][g][q].w;
+          }
+          xs[h][g].x = xs[h][g].x + t.x; xs[h][g].y = xs[h][g].y + t.y;
+          xs[h][g].z = xs[h][g].z + t.z; xs[h][g].w = xs[h][g].w + t.w;
+        }
     }
-    ln_load(0, lx, lpv);
+  };
+  if constexpr (LNP > 0) {
+    const int wt = min(tid, KF / 4 - 1);  // threads past KF / 4 re-read the last group (not stored)
+    wb4[0] = *(const floatx4*)(p.ln.w + wt * 4);
+    wb4[1] = *(const floatx4*)(p.ln.b + wt * 4);
+    ln_issue(0);
+    __builtin_amdgcn_sched_barrier(0);  // these loads stay in front of the weight stream
   }
   if constexpr (AHEAD) {
 #pragma unroll
@@ -266,41 +293,73 @@ __device__ __forceinline__ void gemm_small_dev(const GemmP& p, int bx, int by, i
   }
 
   if constexpr (LNP > 0) {
+    __builtin_amdgcn_sched_barrier(0);  // nothing that waits on the prologue's loads moves above the stream
     static_assert(BM == 16 && DIRECT && KF <= 64 * MAXE && NT == 256, "LayerNorm prologue shape");
-    auto ln_rows = [&](int r0, float (&x)[2][LE], float (&pv)[2][LE][LP]) {
+    float lw[MAXE], lb[MAXE];
+    {  // every thread stores (those past KF / 4 the last group again): a store under a branch
+       // let the compiler sink the loads behind the weight stream
+      const int wt = min(tid, KF / 4 - 1);
+      *(floatx4*)(stg + 16 * KF + wt * 4) = wb4[0];
+      *(floatx4*)(stg + 17 * KF + wt * 4) = wb4[1];
+    }
+    auto ln_rows = [&](int r0) {
+      // this wave's two rows into LDS and back in ln_row's mapping (the wave reads only what it
+      // wrote, so a wave-level fence orders it)
 #pragma unroll
       for (int h = 0; h < 2; h++) {
         const int r = r0 + wave + 4 * h;
         if (r < M) {
-          if constexpr (NPART > 0) {  // reduce_resid_ln_kernel's order: x + (0 + p0 + p1 + ...)
 #pragma unroll
-            for (int i = 0; i < NE; i++) {
-              float t = 0.f;
+          for (int g = 0; g < G; g++) *(floatx4*)(stg + r * KF + g * 256 + lane * 4) = xs[h][g];
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-              for (int q = 0; q < NPART; q++) t += pv[h][i][q];
-              x[h][i] = x[h][i] + t;
-            }
-          }
-          ln_apply_wb(x[h], NE, KF, lw, lb, p.ln.eps);
+      for (int h = 0; h < 2; h++) {
+        const int r = r0 + wave + 4 * h;
+        float x[MAXE];
+        if (r < M) {
+#pragma unroll
+          for (int i = 0; i < NE; i++) x[i] = stg[r * KF + lane + 64 * i];
+          ln_apply_wb(x, NE, KF, lw, lb, p.ln.eps);
           if (bx == 0 && by == 0) {
 #pragma unroll
-            for (int i = 0; i < NE; i++) p.ln.out[(size_t)r * KF + lane + 64 * i] = x[h][i];
+            for (int i = 0; i < NE; i++) p.ln.out[(size_t)r * KF + lane + 64 * i] = x[i];
           }
         } else {
 #pragma unroll
-          for (int i = 0; i < NE; i++) x[h][i] = 0.f;
+          for (int i = 0; i < NE; i++) x[i] = 0.f;
         }
 #pragma unroll
         for (int i = 0; i < NE; i++) {
           const int k = lane + 64 * i;  // chunk k/8 stored at (k/8) ^ (r & 7), as swz
-          sXf[r][(((k >> 3) ^ (r & 7)) << 3) + (k & 7)] = (_Float16)__float2half_rn(x[h][i]);
+          sXf[r][(((k >> 3) ^ (r & 7)) << 3) + (k & 7)] = (_Float16)__float2half_rn(x[i]);
         }
       }
     };
-    ln_rows(0, lx, lpv);
-    float x8[2][LE], pv8[2][LE][LP];
-    ln_load(8, x8, pv8);  // rows 8..15 (no loads when M <= 8)
-    ln_rows(8, x8, pv8);
+    // barriers on LDS only (lgkmcnt): the weight stream stays in flight behind the prologue
+    auto lds_barrier = [&]() {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    lds_barrier();  // the LayerNorm weights are in LDS
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+      lw[i] = stg[16 * KF + lane + 64 * i];
+      lb[i] = stg[17 * KF + lane + 64 * i];
+    }
+    ln_sum();
+    ln_rows(0);
+    if (M > 8) {  // rows 8..15
+      ln_issue(8);
+      ln_sum();
+      ln_rows(8);
+    }
+    lds_barrier();  // every wave is done with the staging before the pieces are decoded there
   }
 
   const int lr = lane & 15, lg = lane >> 4;
