@@ -5,6 +5,7 @@
 
 #include "deq_device.h"
 #include "lle_internal.h"
+#include "mfma_common.h"
 #include "row_device.h"
 
 namespace lle {
@@ -152,6 +153,77 @@ __device__ __forceinline__ void reduce_ln_pool_dev(const float* __restrict__ par
   const int row0 = seq_off ? seq_off[b] : b * L;
   const int ne = D / 64, c0 = 4 * tid;
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (D == 768) {
+    // Two rows per wave at a time with 16-byte loads (rows 4 elements per lane, the partials
+    // summed element-wise in the same order), staged in lnrow and read back in ln_row's element
+    // mapping for the LayerNorm: 30 loads per lane in flight at once instead of 60 per row, which
+    // went past the 63 a wave can have. Same arithmetic, same bits.
+    float wv_[MAXE], bv_[MAXE];
+#pragma unroll
+    for (int i = 0; i < MAXE; i++)
+      if (i < ne) {
+        wv_[i] = w[lane + 64 * i];
+        bv_[i] = bb[lane + 64 * i];
+      }
+    constexpr int G = 3, NEC = 12;  // D = 768
+    for (int i0 = 0; i0 < count; i0 += RLP_ROWS) {
+      for (int k0 = wv; k0 < RLP_ROWS; k0 += 8) {  // wave wv: rows k0 and k0 + 4, then + 8
+        floatx4 xs[2][G], pv[2][G][NCH];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int k = k0 + 4 * h;
+          const int t = row0 + rows[i0 + min(k, count - i0 - 1)];  // past the last row: re-read it
+#pragma unroll
+          for (int g = 0; g < G; g++) {
+              const int j = g * 256 + lane * 4;
+              xs[h][g] = *(const floatx4*)(src + (size_t)t * D + j);
+#pragma unroll
+              for (int c = 0; c < NCH; c++) pv[h][g][c] = *(const floatx4*)(part + ((size_t)c * M + t) * D + j);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int k = k0 + 4 * h;
+#pragma unroll
+          for (int g = 0; g < G; g++) {
+              floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int c = 0; c < NCH; c++) acc += pv[h][g][c];
+              floatx4 x = xs[h][g];
+              x.x = x.x + acc.x; x.y = x.y + acc.y; x.z = x.z + acc.z; x.w = x.w + acc.w;
+              *(floatx4*)&lnrow[k][g * 256 + lane * 4] = x;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int k = k0 + 4 * h;
+          if (i0 + k < count) {
+            float x[MAXE];
+#pragma unroll
+            for (int i = 0; i < NEC; i++) x[i] = lnrow[k][lane + 64 * i];
+            ln_apply_wb(x, NEC, D, wv_, bv_, eps);
+#pragma unroll
+            for (int i = 0; i < NEC; i++) lnrow[k][lane + 64 * i] = x[i];
+          }
+        }
+      }
+      __syncthreads();
+      if (c0 < D) {
+        const int nr = count - i0 < RLP_ROWS ? count - i0 : RLP_ROWS;
+        for (int u = 0; u < nr; u++) {
+          const float4 v = *(const float4*)&lnrow[u][c0];
+          s.x += v.x;
+          s.y += v.y;
+          s.z += v.z;
+          s.w += v.w;
+        }
+      }
+      __syncthreads();
+    }
+  } else {
   for (int i0 = 0; i0 < count; i0 += RLP_ROWS) {
     for (int k = wv; k < RLP_ROWS; k += 4) {  // wave wv: rows i0 + wv, + 4, + 8, + 12
       if (i0 + k < count) {
@@ -192,6 +264,7 @@ __device__ __forceinline__ void reduce_ln_pool_dev(const float* __restrict__ par
       }
     }
     __syncthreads();
+  }
   }
   if (c0 < D) {
     if (count != 0) {
