@@ -1,6 +1,5 @@
 // Attention block as a device function (bidirectional masked multi-head attention, the
-// reference's softmax semantics). The attention kernel (attention.hip) and the persistent
-// small-batch forward (persist.hip) run this same code.
+// reference's softmax semantics), run by the attention kernel (attention.hip).
 #pragma once
 
 #include "lle_internal.h"

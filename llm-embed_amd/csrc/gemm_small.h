@@ -1,6 +1,5 @@
 // Shared pieces of the projection GEMMs: the parameter block, the epilogues and the small-M
-// GEMM as a device function (its kernel in gemm.hip, and the persistent small-batch forward in
-// persist.hip, run the same code, so both produce the same bits).
+// GEMM as a device function (run by the gemm_small kernel in gemm.hip).
 #pragma once
 
 #include "deq_device.h"

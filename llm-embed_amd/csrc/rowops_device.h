@@ -1,6 +1,5 @@
 // Row stages as device functions: the embedding gather + LayerNorm, the pool helpers and the
-// fused last LayerNorm + mean pool of small forwards. The row kernels (rowops.hip) and the
-// persistent small-batch forward (persist.hip) run this same code.
+// fused last LayerNorm + mean pool of small forwards, run by the row kernels (rowops.hip).
 #pragma once
 
 #include "deq_device.h"
