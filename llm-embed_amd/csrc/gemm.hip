@@ -1153,7 +1153,7 @@ __global__ __launch_bounds__(BN * 4) void gemm_small(GemmP p) {
   using SS = SmallShape<FMT, BM, BN, NPIECE, LNP>;
   __shared__ __attribute__((aligned(16))) unsigned char lds[SS::LDS];
   RawSeg wr[SS::NP][SS::WPT];
-  gemm_small_dev<FMT, BM, BN, NPIECE, EPI, DIRECT, LNP, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds, wr);
+  gemm_small_dev<FMT, BM, BN, NPIECE, EPI, DIRECT, LNP>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds, wr);
 }
 
 template <int EPI>

@@ -169,27 +169,9 @@ struct SmallShape {
   static constexpr size_t LDS = SW + SX + SXF;  // bytes, every part a multiple of 16
 };
 
-// The weight segments of block (bx, by)'s pieces, loaded into wr (what gemm_small_dev loads
-// itself when PREW is false); lets a caller issue them early.
-template <int FMT, int BM, int BN, int NPIECE>
-__device__ __forceinline__ void gemm_small_wload(const GemmP& p, int bx, int by,
-                                                 RawSeg (&wr)[SmallShape<FMT, BM, BN, NPIECE, 0>::NP]
-                                                             [SmallShape<FMT, BM, BN, NPIECE, 0>::WPT]) {
-  using SS = SmallShape<FMT, BM, BN, NPIECE, 0>;
-  static_assert(SS::AHEAD, "preloaded pieces need quantised weights");
-  const int tid = threadIdx.x, n0 = bx * BN, kbase = by * NPIECE * SS::PK;
-#pragma unroll
-  for (int pc = 0; pc < NPIECE; pc++)
-#pragma unroll
-    for (int i = 0; i < SS::WPT; i++) {
-      const int u = tid + i * SS::NT;
-      wr[pc][i] = load_seg<FMT>(p.w, n0 + (u >> 4), kbase + pc * SS::PK + (u & 15) * 16);
-    }
-}
-
 // Block (bx, by, bz) of the small-M GEMM, its LDS at `lds` (SmallShape::LDS bytes, 16-byte
-// aligned). PREW: wr already holds the block's weight segments (gemm_small_wload).
-template <int FMT, int BM, int BN, int NPIECE, int EPI, bool DIRECT, int LNP, bool PREW>
+// aligned); wr holds the block's weight segments as they arrive.
+template <int FMT, int BM, int BN, int NPIECE, int EPI, bool DIRECT, int LNP>
 __device__ __forceinline__ void gemm_small_dev(const GemmP& p, int bx, int by, int bz, unsigned char* lds,
                                                RawSeg (&wr)[SmallShape<FMT, BM, BN, NPIECE, LNP>::NP]
                                                            [SmallShape<FMT, BM, BN, NPIECE, LNP>::WPT]) {
@@ -201,7 +183,6 @@ __device__ __forceinline__ void gemm_small_dev(const GemmP& p, int bx, int by, i
   constexpr bool AHEAD = SS::AHEAD;
   constexpr int NP = SS::NP, KF = SS::KF;
   constexpr bool ALLW = SS::ALLW;
-  static_assert(!PREW || AHEAD, "preloaded pieces need quantised weights");
   _Float16(*sW)[BN][LDW] = reinterpret_cast<_Float16(*)[BN][LDW]>(lds);
   _Float16(*sX)[LNP ? 1 : BM][LDW] = reinterpret_cast<_Float16(*)[LNP ? 1 : BM][LDW]>(lds + SS::SW);
   _Float16(*sXf)[LNP ? KF : 8] = reinterpret_cast<_Float16(*)[LNP ? KF : 8]>(lds + SS::SW + SS::SX);
@@ -213,12 +194,10 @@ __device__ __forceinline__ void gemm_small_dev(const GemmP& p, int bx, int by, i
 
   uint4 xr[NP][XPT];
   auto load_piece = [&](int slot, int kb) {
-    if constexpr (!PREW) {
 #pragma unroll
-      for (int i = 0; i < WPT; i++) {
-        const int u = tid + i * NT;
-        wr[slot][i] = load_seg<FMT>(p.w, n0 + (u >> 4), kb + (u & 15) * 16);
-      }
+    for (int i = 0; i < WPT; i++) {
+      const int u = tid + i * NT;
+      wr[slot][i] = load_seg<FMT>(p.w, n0 + (u >> 4), kb + (u & 15) * 16);
     }
     if constexpr (LNP == 0) {
 #pragma unroll
