@@ -956,10 +956,14 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln(GemmP p, const float* __res
 // rowln_finish's. The waits count this wave's younger memory operations exactly: slab s + 1's six
 // DMA instructions and the 24 stores of each of its two rows of slab s - 1 (a skipped row past M
 // stores nothing, which only makes the wait stricter).
-template <int BM>
+// DEFER: the residual rows hold a pending LayerNorm (LnDefer): its weights and the block's row
+// statistics come into LDS with the slab-0 weights, and each residual element read from a slab
+// is first finished with ln_elem, which gives the f32 bits ln_kernel would have stored.
+template <int BM, bool DEFER = false>
 __device__ __forceinline__ void rowln_finish_dma(const floatx4 (&acc)[6][BM / 16], unsigned char* smem, const GemmP& p,
                                                  const float* __restrict__ lnw, const float* __restrict__ lnb,
-                                                 float eps, __half* h16, int m0, int wn, int lane) {
+                                                 float eps, __half* h16, int m0, int wn, int lane, const LnDefer& dfr) {
+  static_assert(!DEFER || BM == 128, "the pending statistics come in whole 128-row blocks");
   constexpr int FB = 6, TN = 96, NE = LN_N / 64, NSL = BM / 16;
   constexpr int SLAB = 16 * LN_RS * 4;  // bytes of one slab buffer
   constexpr int DMA_PER = 6;             // 48 KB-instructions per slab over 8 waves
@@ -989,12 +993,19 @@ __device__ __forceinline__ void rowln_finish_dma(const floatx4 (&acc)[6][BM / 16
   // the LayerNorm weights and biases come into LDS with slab 0 (waves 0-5, one 1 KB part
   // each), so the epilogue has no global loads the compiler's wait counting would have to order
   // against the DMA
+  // (DEFER: then the pending LayerNorm's weights and biases, and the block's 128 rows of
+  // {mean, invStd})
   float* sWB = (float*)(smem + 2 * SLAB);
+  const float* sST = sWB + 4 * LN_N;
   float wv[MAXE], bv[MAXE];
   dma_slab(0);
   if (wn < 6) {
     const int part = wn % 3;
     dma16(rsrc_words(wn < 3 ? lnw : lnb), sWB + (wn / 3) * LN_N + part * 256, lane * 16, part * 1024);
+    if constexpr (DEFER)
+      dma16(rsrc_words(wn < 3 ? dfr.w : dfr.b), sWB + (2 + wn / 3) * LN_N + part * 256, lane * 16, part * 1024);
+  } else if (DEFER && wn == 6) {
+    dma16(rsrc_words(dfr.stats), sWB + 4 * LN_N, lane * 16, m0 * 8);
   }
 #pragma unroll
   for (int s = 0; s < NSL; s++) {
@@ -1006,12 +1017,22 @@ __device__ __forceinline__ void rowln_finish_dma(const floatx4 (&acc)[6][BM / 16
     else
       wait_bar(std::integral_constant<int, ST>{});
     float* buf = slab(s);
+    float2 rs;
+    if constexpr (DEFER) rs = *(const float2*)(sST + (s * 16 + lr) * 2);
 #pragma unroll
     for (int i = 0; i < FB; i++) {
       float* px = buf + lr * LN_RS + wn * TN + i * 16 + lg * 4;
       floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
       v += acc[i][s];  // total = 0 + chunk
-      const floatx4 h = *(const floatx4*)px;
+      floatx4 h = *(const floatx4*)px;
+      if constexpr (DEFER) {
+        const int col = wn * TN + i * 16 + lg * 4;
+        const floatx4 pw = *(const floatx4*)(sWB + 2 * LN_N + col), pb = *(const floatx4*)(sWB + 3 * LN_N + col);
+        h.x = ln_elem(h.x, rs.x, rs.y, pw.x, pb.x);
+        h.y = ln_elem(h.y, rs.x, rs.y, pw.y, pb.y);
+        h.z = ln_elem(h.z, rs.x, rs.y, pw.z, pb.z);
+        h.w = ln_elem(h.w, rs.x, rs.y, pw.w, pb.w);
+      }
       floatx4 x;
       x.x = h.x + v.x; x.y = h.y + v.y; x.z = h.z + v.z; x.w = h.w + v.w;
       *(floatx4*)px = x;
@@ -1050,9 +1071,10 @@ __device__ __forceinline__ void rowln_finish_dma(const floatx4 (&acc)[6][BM / 16
 // 16 rows of 64 bytes; lane L fills slot L % 4 of row L / 4 with logical chunk (L % 4) ^ swr(row))
 // through NS LDS stages (3 x 52 KB for 64 rows, 2 x 56 KB for 128), loads NS - 1 K steps ahead;
 // MFMA order and epilogue as above.
-template <int BM, int NS>
+template <int BM, int NS, bool DEFER = false>
 __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __restrict__ lnw,
-                                                       const float* __restrict__ lnb, float eps, __half* h16) {
+                                                       const float* __restrict__ lnb, float eps, __half* h16,
+                                                       LnDefer dfr) {
   constexpr int WN = 8, TN = LN_N / WN, FB = TN / 16, TB = BM / 16;
   static_assert(NS == 2 || NS == 3, "stages");
   constexpr int W_STAGE = LN_N * LN_KS * 2, X_STAGE = BM * LN_KS * 2, STAGE = W_STAGE + X_STAGE;
@@ -1062,7 +1084,8 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __r
   constexpr int R_BYTES = 32 * LN_RS * 4;
   constexpr int SMEM = NS * STAGE > R_BYTES ? NS * STAGE : R_BYTES;
   static_assert(SMEM <= 160 * 1024, "LDS");
-  static_assert(SMEM >= 2 * 16 * LN_RS * 4 + 2 * LN_N * 4, "LDS of the epilogue's slabs and weights");
+  static_assert(SMEM >= 2 * 16 * LN_RS * 4 + (DEFER ? 4 * LN_N * 4 + BM * 8 : 2 * LN_N * 4),
+                "LDS of the epilogue's slabs and weights");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
   typedef _Float16 Row[LN_KS];
 
@@ -1137,7 +1160,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __r
     stage = stage == NS - 1 ? 0 : stage + 1;
   }
   __syncthreads();  // every stage read: LDS is free for the row staging
-  rowln_finish_dma<BM>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane);
+  rowln_finish_dma<BM, DEFER>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane, dfr);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1396,11 +1419,30 @@ hipError_t launch_gemm_lnx(const GemmArgs& a, int epi, const LnPrologue& ln, hip
   }
 }
 
+// The 128-row full-row kernel's condition (see launch_gemm_resid_ln).
+static bool resid_ln_full_row128(const GemmP& p) {
+  return p.M >= 128 * num_cus() && p.N == LN_N && p.K / kchunk_of(p.K) == 1 && p.K % 64 == 0 && p.w16;
+}
+
+bool gemm_resid_ln_takes_defer(const GemmArgs& a) {
+  const GemmP p = make_params(a);
+  return (int64_t)p.M * p.K * 2 <= INT32_MAX && resid_ln_full_row128(p);
+}
+
+// The split path with the LayerNorm kernel (last case of launch_gemm_resid_ln) at M >= 1024 and
+// with several K chunks: the full-row kernels need one chunk, the partials path M < 1024.
+bool gemm_resid_ln_gives_defer(const GemmArgs& a) {
+  const GemmP p = make_params(a);
+  return (int64_t)p.M * p.K * 2 <= INT32_MAX && p.M >= 1024 && p.K / kchunk_of(p.K) > 1;
+}
+
 hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
-                                hipStream_t st) {
+                                hipStream_t st, const LnDefer* defer_in, float2* stats_out) {
   const GemmP p = make_params(a);
   const int nch = p.K / kchunk_of(p.K);
   if ((int64_t)p.M * p.K * 2 > INT32_MAX) return hipErrorInvalidValue;  // 32-bit buffer offsets
+  if ((defer_in && !gemm_resid_ln_takes_defer(a)) || (stats_out && !gemm_resid_ln_gives_defer(a)))
+    return hipErrorInvalidValue;
   // Without the f16 copy the decoding kernel (weights decoded in the loop, 64-row tiles) runs
   // 128-row tiles on the f16 copy (every format) once they give every CU a block: each block
   // streams the 1.2 MB weight once for twice the rows of the 64-row kernels (measured 0.103
@@ -1415,15 +1457,20 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
   // (16384 rows: 0.055 against 0.064 ms).
   const bool split_mid = p.w16 && p.M >= 1024 && (p.K / KSTEP) % 3 == 0 && p.N % 128 == 0 &&
                          (int64_t)((p.M + 255) / 256) * (p.N / 128) <= num_cus();
-  if (p.M >= 128 * num_cus() && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16) {
-    hipLaunchKernelGGL((gemm_rowln_h<128, 2>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16);
+  if (resid_ln_full_row128(p)) {
+    if (defer_in)
+      hipLaunchKernelGGL((gemm_rowln_h<128, 2, true>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16,
+                         *defer_in);
+    else
+      hipLaunchKernelGGL((gemm_rowln_h<128, 2>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16,
+                         LnDefer{});
     return hipGetLastError();
   }
   // Q8_0 keeps the decoding kernel: its packed decode is cheap and the block streams half the
   // weight bytes (measured 0.114 vs 0.124 ms at 32768 tokens); the K-quants' decode is not cheap
   if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16 && a.w->type != LLE_TYPE_Q8_0 &&
       (p.K / LN_KS) % 3 == 0) {
-    hipLaunchKernelGGL((gemm_rowln_h<64, 3>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16);
+    hipLaunchKernelGGL((gemm_rowln_h<64, 3>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16, LnDefer{});
     return hipGetLastError();
   }
   if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) {
@@ -1445,6 +1492,7 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
   }
   hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, true);
   if (e != hipSuccess) return e;
+  if (stats_out) return launch_ln_stats(p.y, h16, stats_out, w, b, eps, p.M, p.N, st);
   return launch_ln(p.y, h16, w, b, eps, p.M, p.N, st);
 }
 

@@ -82,9 +82,21 @@ struct GemmArgs {
 };
 
 hipError_t launch_gemm(const GemmArgs& a, int epi, hipStream_t st);
-// a.y (= h) += X . W^T, then LayerNorm(h; w, b, eps) into h and h16
+// A LayerNorm left pending by launch_ln_stats: the f32 rows hold its input, stats[t] = {mean,
+// invStd}, and w / b are its weights; the consumer applies ln_elem to each element it reads.
+struct LnDefer {
+  const float* w;
+  const float* b;
+  const float2* stats;  // padded to a multiple of 128 rows (read in whole 128-row blocks)
+};
+// a.y (= h) += X . W^T, then LayerNorm(h; w, b, eps) into h and h16.
+// defer_in: the residual a.y holds a pending LayerNorm (only where gemm_resid_ln_takes_defer).
+// stats_out: leave this LayerNorm pending instead (h16 and stats_out written, h left as the sum;
+// only where gemm_resid_ln_gives_defer).
 hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
-                                hipStream_t st);
+                                hipStream_t st, const LnDefer* defer_in = nullptr, float2* stats_out = nullptr);
+bool gemm_resid_ln_takes_defer(const GemmArgs& a);
+bool gemm_resid_ln_gives_defer(const GemmArgs& a);
 // M <= 16, K = 768: GEMM whose X operand is LN(src [+ ordered sum of nch partials]) computed in
 // every block (ln_row's arithmetic); block 0 also writes that LayerNorm output (f32) to ln_out.
 // Replaces a LayerNorm (or reduce + residual + LayerNorm) kernel in front of the GEMM.
@@ -130,6 +142,9 @@ struct EmbedArgs {
 hipError_t launch_embed_ln(const EmbedArgs& a, hipStream_t st);
 hipError_t launch_ln(float* h, __half* h16, const float* w, const float* b, float eps, int T, int D,
                      hipStream_t st);
+// ln_kernel that leaves the f32 rows as they are and writes h16 and stats[t] = {mean, invStd}
+hipError_t launch_ln_stats(const float* h, __half* h16, float2* stats, const float* w, const float* b, float eps,
+                           int T, int D, hipStream_t st);
 
 struct AttnArgs {
   const __half* q;

@@ -54,6 +54,29 @@ __device__ __forceinline__ void ln_apply_wb(float* x, int ne, int D, const float
     if (i < ne) x[i] = (x[i] - mean) * inv * wv[i] + bv[i];
 }
 
+// ln_apply_wb in two steps, for a LayerNorm whose elementwise step runs later in another kernel:
+// the row's mean and invStd (the same operations in the same order, so the same bits), and the
+// elementwise step (x - mean) * invStd * w + b (never fused: the library is built with
+// -ffp-contract=off).
+__device__ __forceinline__ void ln_mean_inv(const float* x, int ne, int D, float eps, float& mean, float& inv) {
+  float s = 0.f, ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) {
+      s += x[i];
+      ss += x[i] * x[i];
+    }
+  s = wave_sum(s);
+  ss = wave_sum(ss);
+  const float nf = (float)D;
+  mean = s / nf;
+  const float var = ss / nf - mean * mean;
+  inv = (float)(1.0 / sqrt((double)(var + eps)));
+}
+__device__ __forceinline__ float ln_elem(float x, float mean, float inv, float w, float b) {
+  return (x - mean) * inv * w + b;
+}
+
 __device__ __forceinline__ void ln_apply(float* x, int ne, int D, const float* w, const float* b, float eps,
                                          int lane) {
   float wv[MAXE], bv[MAXE];  // issued before the reductions so their latency overlaps them

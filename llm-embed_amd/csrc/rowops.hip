@@ -45,6 +45,41 @@ hipError_t launch_ln(float* h, __half* h16, const float* w, const float* b, floa
   return hipGetLastError();
 }
 
+// ln_kernel with the f32 rows left unnormalised: writes the f16 rows and each row's mean and
+// invStd (stats[t] = {mean, inv}); the next residual consumer applies the elementwise step
+// itself (ln_elem) and gets ln_kernel's f32 bits.
+__global__ __launch_bounds__(256) void ln_stats_kernel(const float* h, __half* h16, float2* stats, const float* w,
+                                                       const float* b, float eps, int T, int D) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int ne = D / 64;
+  const float* row = h + (size_t)t * D;
+  float wv[MAXE], bv[MAXE], x[MAXE];
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) {
+      wv[i] = w[lane + 64 * i];
+      bv[i] = b[lane + 64 * i];
+    }
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) x[i] = row[lane + 64 * i];
+  float mean, inv;
+  ln_mean_inv(x, ne, D, eps, mean, inv);
+  __half* h16row = h16 + (size_t)t * D;
+#pragma unroll
+  for (int i = 0; i < MAXE; i++)
+    if (i < ne) h16row[lane + 64 * i] = __float2half_rn(ln_elem(x[i], mean, inv, wv[i], bv[i]));
+  if (lane == 0) stats[t] = make_float2(mean, inv);
+}
+
+hipError_t launch_ln_stats(const float* h, __half* h16, float2* stats, const float* w, const float* b, float eps,
+                           int T, int D, hipStream_t st) {
+  hipLaunchKernelGGL(ln_stats_kernel, dim3((T + 3) / 4), dim3(256), 0, st, h, h16, stats, w, b, eps, T, D);
+  return hipGetLastError();
+}
+
 // Ordered split-K reduction + residual add + LayerNorm for one row per wave (M <= 64 path);
 // chunk counts: 768-wide chunks of K = 3072 (4) and the other d_ff / d_model ratios listed below.
 // t = 0 + part[0] + part[1] + ... (gemm_reduce's order), h = h + t (the residual epilogue's add),

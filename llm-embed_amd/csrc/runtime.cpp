@@ -511,6 +511,8 @@ static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const
     }
     return LLE_OK;
   }
+  bool pending = false;  // the residual rows hold a LayerNorm left pending (pend)
+  LnDefer pend{};
   for (int l = 0; l < m->n_layer; l++) {
     Layer& ly = m->layers[l];
     GemmArgs g{};
@@ -542,7 +544,8 @@ static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const
       g.x = w.attn;
       g.y = w.h;
       Scope s(m, st, "gemm_out_ln", 2.0 * T * ly.out.N * ly.out.K, wbytes(ly.out) + (double)T * D * (2 + 18), timed);
-      LAUNCH(launch_gemm_resid_ln(g, ly.anw, ly.anb, m->eps, w.h16, st));
+      LAUNCH(launch_gemm_resid_ln(g, ly.anw, ly.anb, m->eps, w.h16, st, pending ? &pend : nullptr));
+      pending = false;
     }
     {
       g.w = &ly.upgate;
@@ -555,8 +558,17 @@ static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const
       g.w = &ly.down;
       g.x = w.ff;
       g.y = w.h;
+      // Large batches leave this LayerNorm pending when the next out projection can finish it
+      // while it reads its residual (same bits): the LayerNorm kernel then writes only the f16
+      // rows and each row's mean and invStd, not the 4-byte rows (a third of its traffic). The
+      // statistics go to the FFN buffer, free from here until the next up / gate projection.
+      GemmArgs nx = g;
+      if (l + 1 < m->n_layer) nx.w = &m->layers[l + 1].out;
+      pending = l + 1 < m->n_layer && gemm_resid_ln_gives_defer(g) && gemm_resid_ln_takes_defer(nx);
+      float2* stats = (float2*)w.ff;
       Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 18), timed);
-      LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, w.h16, st));
+      LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, w.h16, st, nullptr, pending ? stats : nullptr));
+      pend = LnDefer{ly.onw, ly.onb, stats};
     }
   }
   if (d_out) {
