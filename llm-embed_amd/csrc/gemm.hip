@@ -787,10 +787,10 @@ constexpr int LN_N = 768, LN_KS = 32, LN_RS = LN_N + 4;  // LN staging row strid
 // tokens in LDS (row stride 772 floats: conflict-free), then LayerNorm by ln_row with
 // ln_kernel's element-to-lane mapping (wave w: 4 rows per half). Call after a barrier that
 // ends every read of the K-loop stages, which smem overlays.
-template <int BM>
+template <int BM, bool DEFER = false>
 __device__ __forceinline__ void rowln_finish(const floatx4 (&acc)[6][BM / 16], unsigned char* smem, const GemmP& p,
                                              const float* __restrict__ lnw, const float* __restrict__ lnb,
-                                             float eps, __half* h16, int m0, int wn, int lane) {
+                                             float eps, __half* h16, int m0, int wn, int lane, const LnDefer& dfr) {
   constexpr int FB = 6, TN = 96;
   const int lr = lane & 15, lg = lane >> 4, M = p.M;
   float* sR = (float*)smem;
@@ -806,7 +806,15 @@ __device__ __forceinline__ void rowln_finish(const floatx4 (&acc)[6][BM / 16], u
         v += acc[i][j];  // total = 0 + chunk
         floatx4 x = floatx4{0.f, 0.f, 0.f, 0.f};
         if (m < M) {
-          const floatx4 h = *(const floatx4*)(p.y + (size_t)m * LN_N + f);
+          floatx4 h = *(const floatx4*)(p.y + (size_t)m * LN_N + f);
+          if constexpr (DEFER) {  // finish the pending LayerNorm of the residual (ln_elem)
+            const float2 rs = dfr.stats[m];
+            const floatx4 pw = *(const floatx4*)(dfr.w + f), pb = *(const floatx4*)(dfr.b + f);
+            h.x = ln_elem(h.x, rs.x, rs.y, pw.x, pb.x);
+            h.y = ln_elem(h.y, rs.x, rs.y, pw.y, pb.y);
+            h.z = ln_elem(h.z, rs.x, rs.y, pw.z, pb.z);
+            h.w = ln_elem(h.w, rs.x, rs.y, pw.w, pb.w);
+          }
           x.x = h.x + v.x; x.y = h.y + v.y; x.z = h.z + v.z; x.w = h.w + v.w;
         }
         *(floatx4*)&sR[tl * LN_RS + f] = x;
@@ -828,9 +836,10 @@ __device__ __forceinline__ void rowln_finish(const floatx4 (&acc)[6][BM / 16], u
   }
 }
 
-template <int FMT, int BM>
+template <int FMT, int BM, bool DEFER = false>
 __global__ __launch_bounds__(512, 1) void gemm_rowln(GemmP p, const float* __restrict__ lnw,
-                                                     const float* __restrict__ lnb, float eps, __half* h16) {
+                                                     const float* __restrict__ lnb, float eps, __half* h16,
+                                                     LnDefer dfr) {
   constexpr int NT = 512, WN = 8, TN = LN_N / WN, FB = TN / 16, TB = BM / 16;
   constexpr int WU = LN_N * (LN_KS / 16);  // 1536 weight segments per step
   constexpr int WPT = WU / NT;             // 3
@@ -946,7 +955,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln(GemmP p, const float* __res
   step(S1{}, S0{}, kt + 1, false);
   __syncthreads();  // every stage read: LDS is free for the row staging
 
-  rowln_finish<BM>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane);
+  rowln_finish<BM, DEFER>(acc, smem, p, lnw, lnb, eps, h16, m0, wn, lane, dfr);
 }
 
 // Epilogue of the LDS-DMA full-row kernel, in 16-token slabs. Slab s's residual rows
@@ -963,7 +972,9 @@ template <int BM, bool DEFER = false>
 __device__ __forceinline__ void rowln_finish_dma(const floatx4 (&acc)[6][BM / 16], unsigned char* smem, const GemmP& p,
                                                  const float* __restrict__ lnw, const float* __restrict__ lnb,
                                                  float eps, __half* h16, int m0, int wn, int lane, const LnDefer& dfr) {
-  static_assert(!DEFER || BM == 128, "the pending statistics come in whole 128-row blocks");
+  // the statistics come as one 1 KB LDS-DMA from row m0: 128 rows (64-row blocks read the next
+  // 64 rows' too, unused; the statistics buffer extends 128 rows past the last row)
+  static_assert(!DEFER || BM == 128 || BM == 64, "one statistics DMA per block");
   constexpr int FB = 6, TN = 96, NE = LN_N / 64, NSL = BM / 16;
   constexpr int SLAB = 16 * LN_RS * 4;  // bytes of one slab buffer
   constexpr int DMA_PER = 6;             // 48 KB-instructions per slab over 8 waves
@@ -993,7 +1004,7 @@ __device__ __forceinline__ void rowln_finish_dma(const floatx4 (&acc)[6][BM / 16
   // the LayerNorm weights and biases come into LDS with slab 0 (waves 0-5, one 1 KB part
   // each), so the epilogue has no global loads the compiler's wait counting would have to order
   // against the DMA
-  // (DEFER: then the pending LayerNorm's weights and biases, and the block's 128 rows of
+  // (DEFER: then the pending LayerNorm's weights and biases, and the block's rows of
   // {mean, invStd})
   float* sWB = (float*)(smem + 2 * SLAB);
   const float* sST = sWB + 4 * LN_N;
@@ -1084,7 +1095,7 @@ __global__ __launch_bounds__(512, 1) void gemm_rowln_h(GemmP p, const float* __r
   constexpr int R_BYTES = 32 * LN_RS * 4;
   constexpr int SMEM = NS * STAGE > R_BYTES ? NS * STAGE : R_BYTES;
   static_assert(SMEM <= 160 * 1024, "LDS");
-  static_assert(SMEM >= 2 * 16 * LN_RS * 4 + (DEFER ? 4 * LN_N * 4 + BM * 8 : 2 * LN_N * 4),
+  static_assert(SMEM >= 2 * 16 * LN_RS * 4 + (DEFER ? 4 * LN_N * 4 + 1024 : 2 * LN_N * 4),
                 "LDS of the epilogue's slabs and weights");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
   typedef _Float16 Row[LN_KS];
@@ -1419,21 +1430,34 @@ hipError_t launch_gemm_lnx(const GemmArgs& a, int epi, const LnPrologue& ln, hip
   }
 }
 
-// The 128-row full-row kernel's condition (see launch_gemm_resid_ln).
-static bool resid_ln_full_row128(const GemmP& p) {
-  return p.M >= 128 * num_cus() && p.N == LN_N && p.K / kchunk_of(p.K) == 1 && p.K % 64 == 0 && p.w16;
+// Which kernels launch_gemm_resid_ln runs for a call (see the comments there).
+enum class ResidPath { FULL128, FULLH64, FULLDEC, PARTS, SPLIT };
+static ResidPath resid_path(const GemmP& p, int type) {
+  const int nch = p.K / kchunk_of(p.K);
+  const bool split_mid = p.w16 && p.M >= 1024 && (p.K / KSTEP) % 3 == 0 && p.N % 128 == 0 &&
+                         (int64_t)((p.M + 255) / 256) * (p.N / 128) <= num_cus();
+  if (p.M >= 128 * num_cus() && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16) return ResidPath::FULL128;
+  if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16 && type != LLE_TYPE_Q8_0 &&
+      (p.K / LN_KS) % 3 == 0)
+    return ResidPath::FULLH64;
+  if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) return ResidPath::FULLDEC;
+  if (p.M < 1024 && p.part && (nch == 2 || nch == 3 || nch == 4 || nch == 8 || nch == 12)) return ResidPath::PARTS;
+  return ResidPath::SPLIT;
 }
 
+// The full-row kernels can finish a pending LayerNorm of their residual.
 bool gemm_resid_ln_takes_defer(const GemmArgs& a) {
   const GemmP p = make_params(a);
-  return (int64_t)p.M * p.K * 2 <= INT32_MAX && resid_ln_full_row128(p);
+  const ResidPath r = resid_path(p, a.w->type);
+  return (int64_t)p.M * p.K * 2 <= INT32_MAX &&
+         (r == ResidPath::FULL128 || r == ResidPath::FULLH64 || r == ResidPath::FULLDEC);
 }
 
-// The split path with the LayerNorm kernel (last case of launch_gemm_resid_ln) at M >= 1024 and
-// with several K chunks: the full-row kernels need one chunk, the partials path M < 1024.
+// The split path (tile GEMM with the residual epilogue, then the LayerNorm kernel) can leave its
+// LayerNorm pending.
 bool gemm_resid_ln_gives_defer(const GemmArgs& a) {
   const GemmP p = make_params(a);
-  return (int64_t)p.M * p.K * 2 <= INT32_MAX && p.M >= 1024 && p.K / kchunk_of(p.K) > 1;
+  return (int64_t)p.M * p.K * 2 <= INT32_MAX && resid_path(p, a.w->type) == ResidPath::SPLIT;
 }
 
 hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* b, float eps, __half* h16,
@@ -1443,6 +1467,7 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
   if ((int64_t)p.M * p.K * 2 > INT32_MAX) return hipErrorInvalidValue;  // 32-bit buffer offsets
   if ((defer_in && !gemm_resid_ln_takes_defer(a)) || (stats_out && !gemm_resid_ln_gives_defer(a)))
     return hipErrorInvalidValue;
+  const LnDefer dfr = defer_in ? *defer_in : LnDefer{};
   // Without the f16 copy the decoding kernel (weights decoded in the loop, 64-row tiles) runs
   // 128-row tiles on the f16 copy (every format) once they give every CU a block: each block
   // streams the 1.2 MB weight once for twice the rows of the 64-row kernels (measured 0.103
@@ -1455,40 +1480,49 @@ hipError_t launch_gemm_resid_ln(const GemmArgs& a, const float* w, const float* 
   // CUs, the full-row kernels leave CUs idle and the split path is faster (bit-identical rows;
   // config 3's 8192 rows: 0.038 against 0.055 ms); from there on the full-row kernels win
   // (16384 rows: 0.055 against 0.064 ms).
-  const bool split_mid = p.w16 && p.M >= 1024 && (p.K / KSTEP) % 3 == 0 && p.N % 128 == 0 &&
-                         (int64_t)((p.M + 255) / 256) * (p.N / 128) <= num_cus();
-  if (resid_ln_full_row128(p)) {
-    if (defer_in)
-      hipLaunchKernelGGL((gemm_rowln_h<128, 2, true>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16,
-                         *defer_in);
-    else
-      hipLaunchKernelGGL((gemm_rowln_h<128, 2>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16,
-                         LnDefer{});
-    return hipGetLastError();
-  }
-  // Q8_0 keeps the decoding kernel: its packed decode is cheap and the block streams half the
-  // weight bytes (measured 0.114 vs 0.124 ms at 32768 tokens); the K-quants' decode is not cheap
-  if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0 && p.w16 && a.w->type != LLE_TYPE_Q8_0 &&
-      (p.K / LN_KS) % 3 == 0) {
-    hipLaunchKernelGGL((gemm_rowln_h<64, 3>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16, LnDefer{});
-    return hipGetLastError();
-  }
-  if (!split_mid && p.M >= 1024 && p.N == LN_N && nch == 1 && p.K % 64 == 0) {
-    const dim3 grid((p.M + 63) / 64), blk(512);
-    switch (a.w->type) {
-      case LLE_TYPE_Q8_0: hipLaunchKernelGGL((gemm_rowln<8, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
-      case LLE_TYPE_Q4_K: hipLaunchKernelGGL((gemm_rowln<12, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
-      case LLE_TYPE_Q5_K: hipLaunchKernelGGL((gemm_rowln<13, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
-      case LLE_TYPE_Q6_K: hipLaunchKernelGGL((gemm_rowln<14, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
-      case LLE_TYPE_F32: hipLaunchKernelGGL((gemm_rowln<0, 64>), grid, blk, 0, st, p, w, b, eps, h16); break;
-      default: return hipErrorInvalidValue;
+  // Q8_0 keeps the decoding kernel at 64 rows: its packed decode is cheap and the block streams
+  // half the weight bytes (measured 0.114 vs 0.124 ms at 32768 tokens); the K-quants' decode is
+  // not cheap.
+  switch (resid_path(p, a.w->type)) {
+    case ResidPath::FULL128:
+      if (defer_in)
+        hipLaunchKernelGGL((gemm_rowln_h<128, 2, true>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16, dfr);
+      else
+        hipLaunchKernelGGL((gemm_rowln_h<128, 2>), dim3((p.M + 127) / 128), dim3(512), 0, st, p, w, b, eps, h16, dfr);
+      return hipGetLastError();
+    case ResidPath::FULLH64:
+      if (defer_in)
+        hipLaunchKernelGGL((gemm_rowln_h<64, 3, true>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16, dfr);
+      else
+        hipLaunchKernelGGL((gemm_rowln_h<64, 3>), dim3((p.M + 63) / 64), dim3(512), 0, st, p, w, b, eps, h16, dfr);
+      return hipGetLastError();
+    case ResidPath::FULLDEC: {
+      const dim3 grid((p.M + 63) / 64), blk(512);
+#define LLE_ROWLN(F)                                                                                  \
+  do {                                                                                                \
+    if (defer_in)                                                                                     \
+      hipLaunchKernelGGL((gemm_rowln<F, 64, true>), grid, blk, 0, st, p, w, b, eps, h16, dfr);        \
+    else                                                                                              \
+      hipLaunchKernelGGL((gemm_rowln<F, 64>), grid, blk, 0, st, p, w, b, eps, h16, dfr);              \
+  } while (0)
+      switch (a.w->type) {
+        case LLE_TYPE_Q8_0: LLE_ROWLN(8); break;
+        case LLE_TYPE_Q4_K: LLE_ROWLN(12); break;
+        case LLE_TYPE_Q5_K: LLE_ROWLN(13); break;
+        case LLE_TYPE_Q6_K: LLE_ROWLN(14); break;
+        case LLE_TYPE_F32: LLE_ROWLN(0); break;
+        default: return hipErrorInvalidValue;
+      }
+#undef LLE_ROWLN
+      return hipGetLastError();
     }
-    return hipGetLastError();
-  }
-  if (p.M < 1024 && p.part && (nch == 2 || nch == 3 || nch == 4 || nch == 8 || nch == 12)) {
-    hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, false);
-    if (e != hipSuccess) return e;
-    return launch_reduce_resid_ln(p.part, nch, p.M, p.N, p.y, p.y, h16, w, b, eps, st);
+    case ResidPath::PARTS: {
+      hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, false);
+      if (e != hipSuccess) return e;
+      return launch_reduce_resid_ln(p.part, nch, p.M, p.N, p.y, p.y, h16, w, b, eps, st);
+    }
+    case ResidPath::SPLIT:
+      break;
   }
   hipError_t e = launch_epi<EPI_RESID>(a.w->type, p, st, true);
   if (e != hipSuccess) return e;
