@@ -564,7 +564,9 @@ static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const
       // statistics go to the FFN buffer, free from here until the next up / gate projection.
       GemmArgs nx = g;
       if (l + 1 < m->n_layer) nx.w = &m->layers[l + 1].out;
-      pending = l + 1 < m->n_layer && gemm_resid_ln_gives_defer(g) && gemm_resid_ln_takes_defer(nx);
+      // (the full-row kernels read the statistics in whole 128-row blocks: up to 127 rows past T)
+      pending = l + 1 < m->n_layer && (size_t)(T + 128) * sizeof(float2) <= (size_t)T * F * 2 &&
+                gemm_resid_ln_gives_defer(g) && gemm_resid_ln_takes_defer(nx);
       float2* stats = (float2*)w.ff;
       Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 18), timed);
       LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, w.h16, st, nullptr, pending ? stats : nullptr));
