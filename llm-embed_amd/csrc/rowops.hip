@@ -191,9 +191,13 @@ __global__ __launch_bounds__(256) void reduce_ln_pool_kernel(const float* __rest
 hipError_t launch_reduce_ln_pool(const float* part, int nch, int M, const float* src, const float* w, const float* b,
                                  float eps, const int32_t* mask, const int32_t* seq_off, int B, int L, int D,
                                  int out_dim, float* out, hipStream_t st) {
-  if (L > POOL_MAXL || D > 1024 || D % 64 || nch != 4) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(reduce_ln_pool_kernel<4>, dim3(B), dim3(256), 0, st, part, M, src, w, b, eps, mask, seq_off, L,
-                     D, out_dim, out);
+  if (L > POOL_MAXL || D > 1024 || D % 64 || (nch != 4 && nch != 0)) return hipErrorInvalidValue;
+  if (nch == 4)
+    hipLaunchKernelGGL(reduce_ln_pool_kernel<4>, dim3(B), dim3(256), 0, st, part, M, src, w, b, eps, mask, seq_off, L,
+                       D, out_dim, out);
+  else  // no partials: the rows of src are LayerNormed as they are (ln_kernel's input)
+    hipLaunchKernelGGL(reduce_ln_pool_kernel<0>, dim3(B), dim3(256), 0, st, part, M, src, w, b, eps, mask, seq_off, L,
+                       D, out_dim, out);
   return hipGetLastError();
 }
 

@@ -167,7 +167,7 @@ __device__ __forceinline__ void reduce_ln_pool_dev(const float* __restrict__ par
     constexpr int G = 3, NEC = 12;  // D = 768
     for (int i0 = 0; i0 < count; i0 += RLP_ROWS) {
       for (int k0 = wv; k0 < RLP_ROWS; k0 += 8) {  // wave wv: rows k0 and k0 + 4, then + 8
-        floatx4 xs[2][G], pv[2][G][NCH];
+        floatx4 xs[2][G], pv[2][G][NCH > 0 ? NCH : 1];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
           const int k = k0 + 4 * h;
@@ -185,11 +185,13 @@ __device__ __forceinline__ void reduce_ln_pool_dev(const float* __restrict__ par
           const int k = k0 + 4 * h;
 #pragma unroll
           for (int g = 0; g < G; g++) {
-              floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int c = 0; c < NCH; c++) acc += pv[h][g][c];
               floatx4 x = xs[h][g];
-              x.x = x.x + acc.x; x.y = x.y + acc.y; x.z = x.z + acc.z; x.w = x.w + acc.w;
+              if constexpr (NCH > 0) {
+                floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < NCH; c++) acc += pv[h][g][c];
+                x.x = x.x + acc.x; x.y = x.y + acc.y; x.z = x.z + acc.z; x.w = x.w + acc.w;
+              }
               *(floatx4*)&lnrow[k][g * 256 + lane * 4] = x;
             }
         }
@@ -228,7 +230,7 @@ __device__ __forceinline__ void reduce_ln_pool_dev(const float* __restrict__ par
       if (i0 + k < count) {
         const int t = row0 + rows[i0 + k];
         const float* srow = src + (size_t)t * D;
-        float pv[MAXE][NCH], x[MAXE];
+        float pv[MAXE][NCH > 0 ? NCH : 1], x[MAXE];
 #pragma unroll
         for (int i = 0; i < MAXE; i++)
           if (i < ne) {
@@ -237,14 +239,16 @@ __device__ __forceinline__ void reduce_ln_pool_dev(const float* __restrict__ par
 #pragma unroll
             for (int c = 0; c < NCH; c++) pv[i][c] = part[((size_t)c * M + t) * D + j];
           }
+        if constexpr (NCH > 0) {
 #pragma unroll
-        for (int i = 0; i < MAXE; i++)
-          if (i < ne) {
-            float acc = 0.f;
+          for (int i = 0; i < MAXE; i++)
+            if (i < ne) {
+              float acc = 0.f;
 #pragma unroll
-            for (int c = 0; c < NCH; c++) acc += pv[i][c];
-            x[i] = x[i] + acc;
-          }
+              for (int c = 0; c < NCH; c++) acc += pv[i][c];
+              x[i] = x[i] + acc;
+            }
+        }
         ln_apply(x, ne, D, w, bb, eps, lane);
 #pragma unroll
         for (int i = 0; i < MAXE; i++)

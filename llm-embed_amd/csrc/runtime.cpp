@@ -513,6 +513,7 @@ static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const
   }
   bool pending = false;  // the residual rows hold a LayerNorm left pending (pend)
   LnDefer pend{};
+  bool pooled = false;    // the last LayerNorm runs inside the pool
   for (int l = 0; l < m->n_layer; l++) {
     Layer& ly = m->layers[l];
     GemmArgs g{};
@@ -568,12 +569,24 @@ static int forward(lle_model* m, const Workspace& w, const int32_t* d_ids, const
       pending = l + 1 < m->n_layer && (size_t)(T + 128) * sizeof(float2) <= (size_t)T * F * 2 &&
                 gemm_resid_ln_gives_defer(g) && gemm_resid_ln_takes_defer(nx);
       float2* stats = (float2*)w.ff;
+      // Many short sequences: the last LayerNorm runs inside the pool (one block per sequence,
+      // its kept rows normalised 16 at a time in LDS and summed in row order; the same bits as
+      // the LayerNorm kernel + pool), so neither the f32 nor the f16 rows are written
+      pooled = d_out && l + 1 == m->n_layer && B >= 128 && L <= 256 && gemm_resid_ln_gives_defer(g);
       Scope s(m, st, "gemm_down_ln", 2.0 * T * ly.down.N * ly.down.K, wbytes(ly.down) + (double)T * (F * 2 + D * 18), timed);
-      LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, w.h16, st, nullptr, pending ? stats : nullptr));
+      if (pooled)
+        LAUNCH(launch_gemm(g, EPI_RESID, st));
+      else
+        LAUNCH(launch_gemm_resid_ln(g, ly.onw, ly.onb, m->eps, w.h16, st, nullptr, pending ? stats : nullptr));
       pend = LnDefer{ly.onw, ly.onb, stats};
     }
   }
-  if (d_out) {
+  if (pooled) {
+    const Layer& last = m->layers[m->n_layer - 1];
+    Scope s(m, st, "pool", 0, (double)T * D * 4, timed);
+    LAUNCH(launch_reduce_ln_pool(nullptr, 0, T, w.h, last.onw, last.onb, m->eps, d_mask, seq_off, B, L, D, out_dim,
+                                 d_out, st));
+  } else if (d_out) {
     Scope s(m, st, "pool", 0, (double)T * D * 4, timed);
     // the FFN buffer is free by now: it holds the sliced pool's per-sequence means
     LAUNCH(launch_pool(w.h, d_mask, seq_off, B, L, D, out_dim, d_out, (float*)w.ff, (size_t)T * F * 2, st));
